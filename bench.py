@@ -1,0 +1,256 @@
+#!/usr/bin/env python3
+"""Benchmark: MoE-layer decode on one MI355X.
+
+Workload (the full-size decode layer): hidden 2048, expert intermediate 512,
+512 routed experts top-10 + 1 shared expert (intermediate 512), batch 1,
+4-bit affine group-32 experts (uniform nibbles, bf16 scales U(0.005, 0.02),
+bf16 biases U(-0.1, 0.1)), bf16 router N(0, 0.02), bf16 activations N(0, 1);
+every expert resident in one HBM pool at a random slot behind an int32 slot
+table.  A step is one token through one MoE layer (router, slot lookup,
+shared expert, ten routed experts, combine).  Steps cycle through --layers
+distinct layers (48 by default, 48 GB of expert records) so the 256 MB
+Infinity Cache cannot serve repeated weights; inputs are resident in HBM.
+
+value = layer-tokens/s over the timed steps (graph replay of one pass over
+the layers per replay, unless --eager).  roofline: the gate/up kernel (the
+largest HBM consumer) timed with HIP events on its stream in a second pass
+over the same steps; bytes = algorithmic bytes of one launch.  cpu_baseline:
+the C restatement of the same layer (oracle/cmoe.c, OpenMP) on a bounded
+sample of tokens, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "veystrix-core_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def build_stack(spec, layers, device, seed):
+    import torch
+
+    from veymoe import assemble
+    from veymoe.layer import HipSwitchGLU, MoELayer, QuantizedMLP, RouterLinear
+    from veymoe.executor import Q4G32Projection
+    from veymoe.pool import ExpertPool
+
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    layout = spec.layout
+    slots = layers * spec.experts
+    pool = ExpertPool(layout, slots, layers=layers, experts=spec.experts, device=device)
+    view = pool.buffer[pool.header_size:].view(slots, layout.record_stride)
+    chunk = 512
+    for start in range(0, slots, chunk):
+        assemble.random_records_(view[start:start + chunk], layout, gen)
+    perm = torch.randperm(slots, generator=torch.Generator().manual_seed(seed)).numpy()
+    for layer in range(layers):
+        pool.place_all(layer, perm[layer * spec.experts:(layer + 1) * spec.experts])
+    pool.sync_tables()
+
+    def q4(count, out_w, in_w):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (count, out_w, in_w // 8), dtype=torch.int32, device=device,
+                          generator=gen)
+        s = torch.empty((count, out_w, in_w // 32), device=device).uniform_(0.005, 0.02, generator=gen)
+        b = torch.empty((count, out_w, in_w // 32), device=device).uniform_(-0.1, 0.1, generator=gen)
+        return Q4G32Projection(w, s.to(torch.bfloat16), b.to(torch.bfloat16))
+
+    stack = []
+    for layer in range(layers):
+        router = (torch.randn((spec.experts, spec.hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
+        shared = QuantizedMLP(q4(1, spec.shared_inter, spec.hidden), q4(1, spec.shared_inter, spec.hidden),
+                              q4(1, spec.hidden, spec.shared_inter))
+        switch = HipSwitchGLU(spec.hidden, spec.inter, spec.experts, pool=pool, layer_id=layer)
+        stack.append(MoELayer(RouterLinear(router), switch, spec.top_k, shared_expert=shared,
+                              shared_expert_gate=q4(1, 1, spec.hidden)))
+    return stack, pool
+
+
+def algorithmic_bytes(spec):
+    """Per token-layer and per gate/up launch (bytes the algorithm must read/write)."""
+    expert = spec.layout.record_bytes                       # 1.875 * I * H
+    proj = expert // 3                                      # one projection
+    shared = expert if spec.shared_inter else 0
+    seg = spec.hidden // 2 + 2 * (spec.hidden // 32) * 2    # H -> 1 Q4 gate
+    router = spec.experts * spec.hidden * 2
+    xy = 2 * spec.hidden * 2
+    layer = spec.top_k * expert + shared + seg + router + xy + spec.top_k * 8
+    slots = spec.top_k + (1 if spec.shared_inter else 0)
+    gateup = slots * 2 * proj + spec.hidden * 2 + slots * spec.inter * 2
+    down = slots * proj + slots * spec.inter * 2 + spec.hidden * 2
+    return {"layer": layer, "gateup": gateup, "down": down, "router": router + spec.hidden * 2}
+
+
+def cpu_baseline(spec, seed, seconds):
+    """The C restatement on a bounded sample: one layer of the same shape,
+    decode tokens until ``seconds`` of CPU work."""
+    import numpy as np
+
+    from oracle.build import LIB, build
+    from oracle.cmoe import CDecodeLayer, threads
+    from veymoe import synth
+    from veymoe.bf16 import f32_to_bf16_bits
+
+    if not os.path.exists(LIB):
+        build()
+    layout = spec.layout
+    rng = np.random.default_rng(seed)
+    records = rng.integers(0, 256, size=(spec.experts, layout.record_stride), dtype=np.uint8)
+    for proj in ("gate_proj", "up_proj", "down_proj"):
+        for part, (lo, hi) in (("scales", (0.005, 0.02)), ("biases", (-0.1, 0.1))):
+            off, size = layout.offset(proj, part), layout.sizes[(proj, part)]
+            vals = f32_to_bf16_bits(rng.uniform(lo, hi, size=(spec.experts, size // 2)).astype(np.float32))
+            records[:, off:off + size] = vals.view(np.uint8)
+    layer = CDecodeLayer(spec.hidden, spec.inter, spec.experts, spec.top_k, synth.router_weight(spec, seed, 0),
+                         records, layout.record_stride, layout.part_offsets(),
+                         shared=synth.shared_parts(spec, seed, 0))
+    xs = synth.tokens(spec, seed, 64)
+    layer.run(xs[0])
+    count = 0
+    start = time.perf_counter()
+    while True:
+        layer.run(xs[count % len(xs)])
+        count += 1
+        elapsed = time.perf_counter() - start
+        if elapsed >= seconds:
+            break
+    return {"value": round(count / elapsed, 2), "unit": "tok/s", "cores": threads(), "kind": "port",
+            "sample": f"{count} decode tokens through one layer of the same shape ({elapsed:.1f} s), "
+                      f"C restatement oracle/cmoe.c with OpenMP"}
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=24000)
+    parser.add_argument("--warmup", type=int, default=2400)
+    parser.add_argument("--layers", type=int, default=48)
+    parser.add_argument("--seed", type=int, default=2026)
+    parser.add_argument("--eager", action="store_true", help="launch layer by layer instead of graph replay")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(the path is single-GPU; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from veymoe import _lib, synth
+    from veymoe.device import stream_handle
+
+    device = torch.device("cuda:0")
+    spec = synth.CONFIGS["decode"]
+    layers = args.layers
+    steps = max(layers, (args.steps // layers) * layers)
+    warmup = max(layers, (args.warmup // layers) * layers)
+    log(f"building {layers} layers ({layers * spec.experts} expert records, "
+        f"{layers * spec.experts * spec.layout.record_stride / 1e9:.1f} GB)")
+    stack, pool = build_stack(spec, layers, device, args.seed)
+    lib = _lib.lib()
+    x = torch.randn((layers, 1, spec.hidden), device=device).to(torch.bfloat16)
+    out = torch.empty_like(x)
+    inds = torch.empty((layers, 1, spec.top_k), dtype=torch.int32, device=device)
+    scores = torch.empty((layers, 1, spec.top_k), dtype=torch.bfloat16, device=device)
+    call_args = [stack[i].layer_args(x[i], out[i], inds[i], scores[i]) for i in range(layers)]
+    refs = [ctypes.byref(a) for a in call_args]
+    fn = lib.vm_moe_layer
+    stream = torch.cuda.Stream(device=device)
+
+    def one_pass(handle):
+        for ref in refs:
+            rc = fn(ref, handle)
+            if rc:
+                _lib.check(rc)
+
+    with torch.cuda.stream(stream):
+        handle = stream_handle(stream)
+        for _ in range(warmup // layers):
+            one_pass(handle)
+        torch.cuda.synchronize()
+        graph = None
+        if not args.eager:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                one_pass(stream_handle(torch.cuda.current_stream()))
+            for _ in range(4):
+                graph.replay()
+            torch.cuda.synchronize()
+        log(f"timing {steps} steps ({'graph' if graph is not None else 'eager'})")
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps // layers):
+            if graph is not None:
+                graph.replay()
+            else:
+                one_pass(handle)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+        ms_per_step = elapsed * 1e3 / steps
+
+        # roofline pass: same steps, eager, every kernel bracketed by HIP events on its stream
+        lib.vm_timing_reset()
+        lib.vm_timing_enable(1)
+        for _ in range(steps // layers):
+            one_pass(handle)
+        torch.cuda.synchronize()
+        lib.vm_timing_enable(0)
+    kernels = {}
+    for name in ("router", "gateup", "down"):
+        total, launches = ctypes.c_double(), ctypes.c_uint64()
+        _lib.check(lib.vm_timing_read(name.encode(), ctypes.byref(total), ctypes.byref(launches)))
+        kernels[name] = {"avg_us": round(total.value * 1e3 / max(1, launches.value), 3),
+                         "launches": int(launches.value)}
+    nbytes = algorithmic_bytes(spec)
+    for name in kernels:
+        kernels[name]["bytes"] = nbytes[name]
+        kernels[name]["gbps"] = round(nbytes[name] / (kernels[name]["avg_us"] * 1e3), 1)
+    gateup = kernels["gateup"]
+    roofline = {"bound": "hbm", "kernel": "gateup (routed + shared gate/up Q4 GEMV + SwiGLU)",
+                "achieved": gateup["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(gateup["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None}
+    result = {
+        "metric": "MoE-layer decode tok/s + achieved HBM GB/s (% peak); prefill tok/s at 2048",
+        "value": round(steps / elapsed, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode layer: hidden 2048, inter 512, 512 experts top-10 + shared (inter 512), "
+                               "batch 1, Q4/G32 experts in an HBM pool behind an int32 slot table",
+                   "layers_cycled": layers, "pool_gb": round(pool.buffer.numel() / 1e9, 2),
+                   "launch": "hipgraph" if graph is not None else "eager",
+                   "parallelism": "single GPU"},
+        "layer_bytes": nbytes["layer"],
+        "layer_gbps": round(nbytes["layer"] / (ms_per_step * 1e6), 1),
+        "layer_frac_of_hbm_peak": round(nbytes["layer"] / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+        "kernels": kernels,
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(spec, args.seed, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,269 @@
+/*
+ * veymoe.h - C ABI of the MI355X (gfx950) routed-expert MoE layer.
+ *
+ * One SwiGLU mixture-of-experts layer with 4-bit affine, group-32 quantized
+ * experts in the MLX packed layout:
+ *   weight  uint32 [E, out, in/8]    nibble k of a row sits at bits 4*(k&7) of word k>>3
+ *   scales  bf16   [E, out, in/32]   (passed as uint16 bit patterns)
+ *   biases  bf16   [E, out, in/32]
+ *   dequantized w = scale * q + bias
+ *
+ * Every pointer is a DEVICE pointer unless the field says "host".  The caller
+ * owns all memory; the library never allocates or frees caller memory.  Calls
+ * are asynchronous on the given HIP stream.  Return value: 0 on success or a
+ * negative VM_E* code; the message of the last failure on the calling thread
+ * is available from vm_last_error().
+ *
+ * Reference interfaces (joyboyreturns/Veystrix-Core) these entry points replace:
+ *   vm_moe_execute     MetalMoEExecutor.execute         models/flashnext/metal_runtime.py:799-974
+ *                      flashnext_native_moe_execute     models/flashnext/tests/bench/metal_runtime_native.mm:258-395
+ *   vm_router_topk     router softmax/top-k/renorm      models/flashnext/adaptive_topk.py:59-65,257-262
+ *                                                       models/flashnext/compiled.py:61-71
+ *   vm_moe_layer       _moe_call decode branch          models/flashnext/adaptive_topk.py:54-293 (rows <= 8)
+ *   vm_moe_grouped     _one_pass/_issue gather_qmm path models/flashnext/expert_cache.py:1949-2037 (rows > 8)
+ *   vm_weighted_combine weighted_combine                models/flashnext/metal_runtime.py:145-191
+ *   vm_pool_stage      ExpertPool.fill/_fill_part       models/flashnext/expert_pool.py:201-220,258-287
+ *   vm_available       flashnext_native_available       metal_runtime_native.mm:196-201
+ *   vm_last_error      flashnext_native_get_last_error  metal_runtime_native.mm:203-209
+ */
+#ifndef VEYMOE_H
+#define VEYMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VM_ABI_VERSION 1
+
+/* status codes (0 = ok) */
+#define VM_OK 0
+#define VM_EINVAL -1      /* malformed argument or shape contract violation */
+#define VM_EUNSUPPORTED -2 /* valid but not implemented for this shape */
+#define VM_EHIP -3        /* a HIP runtime call failed */
+#define VM_EWORKSPACE -4  /* workspace too small */
+
+/* element types of activations, scores and outputs */
+#define VM_BF16 0
+#define VM_F32 1
+
+/* route words (uint32): bit 31 set -> record `word & 0x7fffffff` of the pool
+ * view; clear -> expert index into the dense projection arrays.  When a slot
+ * table is given, route words are expert ids and the table maps each to a pool
+ * slot (-1 = not resident).  Same encoding as the reference's SLOT_BIT
+ * (models/flashnext/expert_pool.py:44, metal_runtime.py:198-228). */
+#define VM_SLOT_BIT 0x80000000u
+
+/* record parts, in the order of the reference's expert-major record
+ * (models/flashnext/slab_pack.py:96-149, expert_pool.py:45-49) */
+enum {
+  VM_PART_GATE_W = 0, VM_PART_GATE_S, VM_PART_GATE_B,
+  VM_PART_UP_W, VM_PART_UP_S, VM_PART_UP_B,
+  VM_PART_DOWN_W, VM_PART_DOWN_S, VM_PART_DOWN_B,
+  VM_PARTS
+};
+
+/* One quantized projection stored as dense expert-major arrays.  All three
+ * pointers may be NULL when every route addresses the pool. */
+typedef struct VmQ4Proj {
+  const uint32_t* weight; /* [E, out, in/8] */
+  const uint16_t* scales; /* [E, out, in/group] bf16 bits */
+  const uint16_t* biases; /* [E, out, in/group] bf16 bits */
+} VmQ4Proj;
+
+/* A byte region of fixed-stride expert records (the expert pool, or a slab
+ * pack: models/flashnext/expert_pool.py:78-117).  Record r starts at
+ * base + header_size + r * record_stride (64-bit offsets). */
+typedef struct VmPoolView {
+  const uint8_t* base;
+  uint64_t header_size;
+  uint64_t record_stride;
+  uint64_t part_offset[VM_PARTS];
+  uint32_t records; /* records addressable through this view */
+  uint32_t reserved;
+} VmPoolView;
+
+/* vm_moe_execute: gate projection, up projection + SwiGLU, down projection and,
+ * when `scores` is given, the router-score combine plus an optional shared
+ * term.  Mirrors MetalMoEExecutor.execute(x, routes, projections, scores=,
+ * slab_pack=, shared_y=, shared=, shared_gate=, pool_activation=, return_all=).
+ *
+ *   x            [tokens, hidden]              act_dtype
+ *   routes       [tokens, slots] uint32 route words
+ *   slot_table   optional [expert_count] int32 (see VM_SLOT_BIT)
+ *   scores       optional [tokens, slots]      score_dtype
+ *   shared_y     optional [tokens, hidden]     act_dtype  (added after the combine)
+ *   shared       optional [tokens, hidden]     act_dtype  } added as shared*shared_gate,
+ *   shared_gate  optional [tokens]             act_dtype  } rounded to act_dtype
+ *   activation_in  optional [tokens, slots, inter] act_dtype: precomputed SwiGLU
+ *                  activations (the reference's pool_activation); skips gate/up
+ *   activation_out optional [tokens, slots, inter]: receives the activations
+ *   gate_out/up_out optional [tokens, slots, inter]: raw projections (return_all)
+ *   output       [tokens, hidden] when scores != NULL, else [tokens, slots, hidden];
+ *                may be NULL when activation_out is given: gate/up/SwiGLU only
+ *                (the reference's pool_activations, metal_runtime.py:783-797)
+ *   status       optional device uint32: OR-ed with 1 when a route or slot is
+ *                out of range (that slot then contributes zeros)
+ *   workspace    device scratch of at least vm_moe_execute_workspace() bytes
+ */
+typedef struct VmMoeArgs {
+  const void* x;
+  VmQ4Proj gate, up, down;
+  VmPoolView pool;
+  VmPoolView stream; /* optional: routes without VM_SLOT_BIT address record
+                        `word` here instead of the dense arrays (the reference's
+                        stream pack, metal_runtime.py:202-208); header_size is
+                        normally 0 */
+  const uint32_t* routes;
+  const int32_t* slot_table;
+  const void* scores;
+  const void* shared_y;
+  const void* shared;
+  const void* shared_gate;
+  const void* activation_in;
+  void* activation_out;
+  void* gate_out;
+  void* up_out;
+  void* output;
+  uint32_t* status;
+  void* workspace;
+  uint64_t workspace_bytes;
+  uint32_t tokens, slots, hidden_size, inter_size, expert_count, group_size;
+  uint32_t act_dtype, score_dtype;
+} VmMoeArgs;
+
+/* vm_router_topk: logits = x . router_weight^T (+ optional fp32 logit bias),
+ * rounded to act_dtype; gates = softmax in fp32, rounded to act_dtype; the
+ * top_k gates by (value descending, expert index ascending); scores = gates of
+ * the selection divided by their sum, each step rounded to act_dtype.
+ *   inds   [tokens, top_k] int32 out, in selection order
+ *   scores [tokens, top_k] act_dtype out (renormalised)
+ *   gates  optional [tokens, expert_count] act_dtype out (full softmax) */
+typedef struct VmRouterArgs {
+  const void* x;
+  const uint16_t* weight; /* [expert_count, hidden] bf16 bits */
+  const float* logit_bias; /* optional [expert_count] */
+  int32_t* inds;
+  void* scores;
+  void* gates;
+  void* workspace;
+  uint64_t workspace_bytes;
+  uint32_t tokens, hidden_size, expert_count, top_k;
+  uint32_t act_dtype;
+  float renorm_blend; /* the reference's FLASHNEXT_RENORM_BLEND; 1 = plain renorm */
+} VmRouterArgs;
+
+/* vm_moe_layer: the whole decode layer (tokens <= VM_LAYER_MAX_TOKENS):
+ * router top-k, device-side expert -> pool slot resolution through
+ * slot_table, the shared expert (gate/up/SwiGLU/down) and its sigmoid gate,
+ * the routed experts, and the fused combine
+ *   y = round(round(sum_j round(down_j) * score_j) + round(sigmoid(g_s) * shared)).
+ * Routed experts come from the pool view (slot_table) or, when slot_table is
+ * NULL, from the dense arrays in `gate/up/down` indexed by expert id.
+ * shared_inter == 0 means no shared expert. */
+#define VM_LAYER_MAX_TOKENS 8
+typedef struct VmLayerArgs {
+  const void* x;                 /* [tokens, hidden] */
+  void* output;                  /* [tokens, hidden] */
+  const uint16_t* router_weight; /* [expert_count, hidden] bf16 */
+  const float* router_bias;      /* optional [expert_count] */
+  VmQ4Proj gate, up, down;       /* dense routed experts (used when slot_table == NULL) */
+  VmPoolView pool;
+  const int32_t* slot_table;     /* [expert_count] or NULL */
+  VmQ4Proj shared_gate_proj, shared_up_proj, shared_down_proj; /* [1, ...] */
+  VmQ4Proj shared_expert_gate;   /* [1, 1, hidden/8]: the H -> 1 quantized gate */
+  int32_t* inds_out;             /* optional [tokens, top_k] */
+  void* scores_out;              /* optional [tokens, top_k] act_dtype */
+  uint32_t* status;              /* optional, see VmMoeArgs */
+  void* workspace;
+  uint64_t workspace_bytes;
+  uint32_t tokens, hidden_size, inter_size, shared_inter, expert_count, top_k, group_size;
+  uint32_t act_dtype;
+  float renorm_blend;
+  uint32_t phases; /* VM_PHASE_* bits; 0 means both.  A router-only call leaves
+                      inds/scores (inds_out/scores_out or the workspace) for a
+                      later experts-only call with the same workspace, so the
+                      host can resolve pool misses in between. */
+} VmLayerArgs;
+#define VM_PHASE_ROUTER 1u
+#define VM_PHASE_EXPERTS 2u
+
+/* vm_moe_grouped: the batched/prefill path for any token count.  Token-by-
+ * expert sort (histogram -> scan -> scatter) on the device, then per-expert
+ * grouped gate/up/SwiGLU and down over each expert's rows, then the combine.
+ * combine_mode 0: fused form (fp32 sum of round(down)*score, as vm_moe_layer)
+ * combine_mode 1: generic form of adaptive_topk.py:275-278,
+ *   y = round(round(sum_j round(round(down_j) * score_j)) + shared_y)
+ * Routes are expert ids resolved through slot_table, or dense indices. */
+typedef struct VmGroupedArgs {
+  const void* x;                 /* [tokens, hidden] */
+  const int32_t* inds;           /* [tokens, top_k] expert ids */
+  const void* scores;            /* [tokens, top_k] act_dtype */
+  VmQ4Proj gate, up, down;
+  VmPoolView pool;
+  const int32_t* slot_table;
+  const void* shared_y;          /* optional [tokens, hidden] act_dtype */
+  void* output;                  /* [tokens, hidden] */
+  uint32_t* status;
+  void* workspace;
+  uint64_t workspace_bytes;
+  uint32_t tokens, top_k, hidden_size, inter_size, expert_count, group_size;
+  uint32_t act_dtype, combine_mode;
+} VmGroupedArgs;
+
+int vm_abi_version(void);
+/* 1 when a gfx950 device is usable by this library, else 0. */
+int vm_available(void);
+/* Copies the calling thread's last error message (NUL-terminated). */
+int vm_last_error(char* buf, size_t len);
+
+uint64_t vm_moe_execute_workspace(uint32_t tokens, uint32_t slots, uint32_t inter_size, uint32_t act_dtype);
+int vm_moe_execute(const VmMoeArgs* args, void* stream);
+
+uint64_t vm_router_workspace(uint32_t tokens, uint32_t expert_count);
+int vm_router_topk(const VmRouterArgs* args, void* stream);
+
+uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t inter_size,
+                                uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype);
+int vm_moe_layer(const VmLayerArgs* args, void* stream);
+
+uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size,
+                                  uint32_t inter_size, uint32_t expert_count, uint32_t act_dtype);
+int vm_moe_grouped(const VmGroupedArgs* args, void* stream);
+
+/* out[t, h] = sum_j expert_outputs[t, j, h] * scores[t, j] in fp32, written in
+ * act_dtype; the normal form of weighted_combine (metal_runtime.py:145-191). */
+int vm_weighted_combine(const void* expert_outputs, const void* scores, void* out,
+                        uint32_t tokens, uint32_t slots, uint32_t hidden_size,
+                        uint32_t act_dtype, uint32_t score_dtype, void* stream);
+
+/* Miss staging: copy `count` whole expert records from pinned host memory
+ * (src_host + src_index[i] * src_stride) to pool record dst_slot[i]
+ * (pool_base + header_size + dst_slot[i] * record_stride), record_bytes each,
+ * with hipMemcpyAsync on `stream`.  src_index and dst_slot are HOST arrays;
+ * indices must be below src_records / pool_records.  Runs that are
+ * consecutive on both sides are merged into one copy, as the reference merges
+ * consecutive rows into one preadv (expert_pool.py:207-212).
+ * Replaces the nine per-part preadv rows of ExpertPool.fill
+ * (expert_pool.py:258-287) with one DMA per record run. */
+int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride, uint64_t pool_records,
+                  const void* src_host, uint64_t src_stride, uint64_t src_records, uint64_t record_bytes,
+                  const int64_t* src_index, const int64_t* dst_slot, uint32_t count,
+                  void* stream);
+
+/* Per-kernel event timing over a window of calls (for rooflines).  While
+ * enabled, every kernel the library launches is bracketed by hipEvents on its
+ * stream; vm_timing_read returns the summed milliseconds and launch count of
+ * the kernel family `name` ("router", "gateup", "down", "grouped_gateup",
+ * "grouped_down", "sort", "combine"). */
+int vm_timing_enable(int enabled);
+int vm_timing_read(const char* name, double* total_ms, uint64_t* launches);
+int vm_timing_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VEYMOE_H */

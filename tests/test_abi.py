@@ -1,0 +1,122 @@
+"""The C ABI library: it loads, exports every declared symbol, its struct
+layouts agree with the ctypes mirror, and its argument checks reject bad
+calls before touching a device (no GPU needed)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from veymoe import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "veymoe.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|uint64_t)\s+(vm_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = _declared()
+    assert len(names) >= 15
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES)
+    assert lib.vm_abi_version() == 1
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    structs = {
+        "VmQ4Proj": _lib.VmQ4Proj, "VmPoolView": _lib.VmPoolView, "VmMoeArgs": _lib.VmMoeArgs,
+        "VmRouterArgs": _lib.VmRouterArgs, "VmLayerArgs": _lib.VmLayerArgs, "VmGroupedArgs": _lib.VmGroupedArgs,
+    }
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
+    for name, cls in structs.items():
+        lines.append(f'printf("{name} size %zu\\n", sizeof({name}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{name}.{field} %zu\\n", offsetof({name}, {field}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split("\n")
+    c_values = dict(line.rsplit(" ", 1) for line in out if line)
+    for name, cls in structs.items():
+        assert int(c_values[f"{name} size"]) == ctypes.sizeof(cls), name
+        for field, _ in cls._fields_:
+            assert int(c_values[f"{name}.{field}"]) == getattr(cls, field).offset, (name, field)
+
+
+def _exec_args(**kw):
+    a = _lib.VmMoeArgs()
+    a.x = 256
+    a.routes = 512
+    a.output = 768
+    a.gate = _lib.VmQ4Proj(1024, 1040, 1056)
+    a.up = _lib.VmQ4Proj(1024, 1040, 1056)
+    a.down = _lib.VmQ4Proj(1024, 1040, 1056)
+    a.tokens, a.slots, a.hidden_size, a.inter_size = 1, 2, 64, 64
+    a.expert_count, a.group_size = 4, 32
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,message", [
+    ("group_size", 64, _lib.VM_EUNSUPPORTED, "group_size"),
+    ("tokens", 0, _lib.VM_EINVAL, "tokens"),
+    ("slots", 11, _lib.VM_EINVAL, "slots"),
+    ("hidden_size", 48, _lib.VM_EINVAL, "group aligned"),
+    ("act_dtype", 7, _lib.VM_EINVAL, "dtype"),
+    ("x", None, _lib.VM_EINVAL, "required"),
+    ("shared", 2048, _lib.VM_EINVAL, "together"),
+])
+def test_execute_rejects_bad_arguments_without_a_device(field, value, code, message):
+    a = _exec_args(**{field: value})
+    rc = _lib.lib().vm_moe_execute(ctypes.byref(a), None)
+    assert rc == code
+    assert message in _lib.last_error()
+
+
+def test_execute_needs_workspace():
+    a = _exec_args(scores=4096, workspace=None, workspace_bytes=0)
+    assert _lib.lib().vm_moe_execute(ctypes.byref(a), None) == _lib.VM_EWORKSPACE
+
+
+def test_router_and_layer_bounds():
+    lib = _lib.lib()
+    r = _lib.VmRouterArgs()
+    r.tokens, r.hidden_size, r.expert_count, r.top_k = 1, 64, 513, 4
+    assert lib.vm_router_topk(ctypes.byref(r), None) == _lib.VM_EINVAL
+    r.expert_count, r.top_k = 4, 5
+    assert lib.vm_router_topk(ctypes.byref(r), None) == _lib.VM_EINVAL
+    assert "top_k cannot exceed" in _lib.last_error()
+    layer = _lib.VmLayerArgs()
+    layer.tokens, layer.hidden_size, layer.expert_count, layer.top_k = 9, 64, 8, 2
+    layer.inter_size, layer.group_size = 64, 32
+    assert lib.vm_moe_layer(ctypes.byref(layer), None) == _lib.VM_EINVAL
+
+
+def test_pool_stage_checks_indices_before_copying():
+    lib = _lib.lib()
+    src = (ctypes.c_int64 * 1)(5)
+    dst = (ctypes.c_int64 * 1)(0)
+    rc = lib.vm_pool_stage(4096, 4096, 4096, 2, 8192, 4096, 4, 4096, src, dst, 1, None)
+    assert rc == _lib.VM_EINVAL and "src_index" in _lib.last_error()
+    src[0], dst[0] = 0, 2
+    rc = lib.vm_pool_stage(4096, 4096, 4096, 2, 8192, 4096, 4, 4096, src, dst, 1, None)
+    assert rc == _lib.VM_EINVAL and "dst_slot" in _lib.last_error()
+    assert lib.vm_pool_stage(None, 0, 0, 0, None, 0, 0, 0, src, dst, 0, None) == _lib.VM_OK
+
+
+def test_library_has_no_cpu_fallback_symbols():
+    """The product library holds only GPU entry points: every compute call
+    takes a stream and runs HIP kernels."""
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert {n for n in exported if n.startswith("vm_")} == set(_declared())

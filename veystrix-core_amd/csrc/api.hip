@@ -1,0 +1,561 @@
+// C ABI of libveymoe: argument validation, workspace layout, launch order and
+// per-kernel event timing.  Shape contracts follow MetalMoEExecutor
+// (models/flashnext/metal_runtime.py:430-461 and :837-895); status codes and
+// the thread-local last error follow the reference's native executor
+// (models/flashnext/tests/bench/metal_runtime_native.mm:196-209).
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/veymoe.h"
+#include "vm_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(VM_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+constexpr uint32_t kMaxTopK = 10;       // MAX_TOP_K, metal_runtime.py:28
+constexpr uint32_t kMaxExperts = 512;   // MAX_EXPERTS, metal_runtime.py:27
+constexpr uint32_t kMaxWidth = 16384;   // MAX_WIDTH, metal_runtime.py:29
+constexpr uint64_t kAlign = 256;
+
+uint64_t align_up(uint64_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+uint32_t act_bytes(uint32_t dtype) { return dtype == VM_BF16 ? 2u : 4u; }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+vm::ProjPtrs to_ptrs(const VmQ4Proj& q) { return vm::ProjPtrs{q.weight, q.scales, q.biases}; }
+
+vm::PoolDev to_pool(const VmPoolView& v) {
+  vm::PoolDev d{};
+  d.base = v.base;
+  d.header = v.header_size;
+  d.stride = v.record_stride;
+  for (int i = 0; i < VM_PARTS; ++i) d.off[i] = v.part_offset[i];
+  d.records = v.base != nullptr ? v.records : 0;
+  return d;
+}
+
+bool proj_ok(const VmQ4Proj& q) {
+  if (q.weight == nullptr) return q.scales == nullptr && q.biases == nullptr;
+  return q.scales != nullptr && q.biases != nullptr && aligned16(q.weight);
+}
+
+int check_pool(const VmPoolView& v, uint32_t hidden, uint32_t inter) {
+  if (v.base == nullptr) return VM_OK;
+  // every part must fit inside the record and keep 16-byte alignment of the words
+  const uint64_t sizes[VM_PARTS] = {
+      uint64_t(inter) * hidden / 2, uint64_t(inter) * (hidden / 32) * 2, uint64_t(inter) * (hidden / 32) * 2,
+      uint64_t(inter) * hidden / 2, uint64_t(inter) * (hidden / 32) * 2, uint64_t(inter) * (hidden / 32) * 2,
+      uint64_t(hidden) * inter / 2, uint64_t(hidden) * (inter / 32) * 2, uint64_t(hidden) * (inter / 32) * 2};
+  for (int i = 0; i < VM_PARTS; ++i) {
+    if (v.part_offset[i] + sizes[i] > v.record_stride)
+      return fail(VM_EINVAL, "pool part %d (offset %llu, %llu bytes) exceeds the record stride %llu", i,
+                  (unsigned long long)v.part_offset[i], (unsigned long long)sizes[i],
+                  (unsigned long long)v.record_stride);
+  }
+  const uint64_t wparts[3] = {v.part_offset[0], v.part_offset[3], v.part_offset[6]};
+  for (uint64_t off : wparts)
+    if ((v.header_size + off) % 16 || v.record_stride % 16)
+      return fail(VM_EINVAL, "pool weight parts must be 16-byte aligned");
+  if (!aligned16(v.base)) return fail(VM_EINVAL, "pool base must be 16-byte aligned");
+  return VM_OK;
+}
+
+// ------------------------------------------------------------ timing ----
+
+struct Timing {
+  std::mutex mu;
+  bool enabled = false;
+  struct Pending {
+    hipEvent_t start, end;
+  };
+  std::map<std::string, std::vector<Pending>> pending;
+  std::map<std::string, std::pair<double, uint64_t>> totals;
+  std::vector<hipEvent_t> free_events;
+  // last begun event per family (launches are issued from one thread)
+  std::map<std::string, hipEvent_t> open;
+
+  hipEvent_t get() {
+    if (!free_events.empty()) {
+      hipEvent_t e = free_events.back();
+      free_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+
+Timing& timing() {
+  static Timing t;
+  return t;
+}
+
+int drain_timing(Timing& t) {
+  for (auto& kv : t.pending) {
+    auto& tot = t.totals[kv.first];
+    for (auto& pe : kv.second) {
+      hipError_t e = hipEventSynchronize(pe.end);
+      if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+      float ms = 0.0f;
+      e = hipEventElapsedTime(&ms, pe.start, pe.end);
+      if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+      tot.first += ms;
+      tot.second += 1;
+      t.free_events.push_back(pe.start);
+      t.free_events.push_back(pe.end);
+    }
+    kv.second.clear();
+  }
+  return VM_OK;
+}
+
+}  // namespace
+
+namespace vm {
+
+void timing_begin(const char* family, hipStream_t stream) {
+  Timing& t = timing();
+  if (!t.enabled) return;
+  std::lock_guard<std::mutex> lock(t.mu);
+  hipEvent_t e = t.get();
+  if (e == nullptr) return;
+  hipEventRecord(e, stream);
+  t.open[family] = e;
+}
+
+void timing_end(const char* family, hipStream_t stream) {
+  Timing& t = timing();
+  if (!t.enabled) return;
+  std::lock_guard<std::mutex> lock(t.mu);
+  auto it = t.open.find(family);
+  if (it == t.open.end()) return;
+  hipEvent_t e = t.get();
+  if (e == nullptr) return;
+  hipEventRecord(e, stream);
+  t.pending[family].push_back({it->second, e});
+  t.open.erase(it);
+}
+
+}  // namespace vm
+
+extern "C" {
+
+int vm_abi_version(void) { return VM_ABI_VERSION; }
+
+int vm_available(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+    fail(VM_EHIP, "no HIP device is visible");
+    return 0;
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return 0;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+    fail(VM_EUNSUPPORTED, "device %d is %s; this library is built for gfx950", dev, prop.gcnArchName);
+    return 0;
+  }
+  return 1;
+}
+
+int vm_last_error(char* buf, size_t len) {
+  if (buf == nullptr || len == 0) return VM_EINVAL;
+  std::strncpy(buf, g_last_error.c_str(), len - 1);
+  buf[len - 1] = '\0';
+  return VM_OK;
+}
+
+// ------------------------------------------------------------ execute ---
+
+uint64_t vm_moe_execute_workspace(uint32_t tokens, uint32_t slots, uint32_t inter_size, uint32_t act_dtype) {
+  return align_up(uint64_t(tokens) * slots * inter_size * act_bytes(act_dtype)) + kAlign;
+}
+
+int vm_moe_execute(const VmMoeArgs* a, void* stream_ptr) {
+  if (a == nullptr) return fail(VM_EINVAL, "null arguments");
+  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const uint32_t T = a->tokens, K = a->slots, H = a->hidden_size, I = a->inter_size;
+  if (a->act_dtype > VM_F32 || a->score_dtype > VM_F32) return fail(VM_EINVAL, "unknown dtype");
+  if (a->group_size != 32) return fail(VM_EUNSUPPORTED, "group_size must be 32");
+  if (T == 0) return fail(VM_EINVAL, "tokens must be positive");
+  if (K == 0 || K > kMaxTopK) return fail(VM_EINVAL, "slots must be in 1..%u", kMaxTopK);
+  if (a->expert_count == 0 || a->expert_count > 0x7fffffffu) return fail(VM_EINVAL, "expert_count must be positive");
+  if (H == 0 || I == 0 || H % 32 || I % 32)
+    return fail(VM_EINVAL, "Q4/G32 projection inputs must be group aligned");
+  if (I > kMaxWidth) return fail(VM_EINVAL, "gate and up projection widths must match the bound");
+  if (a->x == nullptr || a->routes == nullptr) return fail(VM_EINVAL, "x and routes are required");
+  if (a->output == nullptr && a->activation_out == nullptr)
+    return fail(VM_EINVAL, "an output or an activation output is required");
+  if (a->output == nullptr && a->activation_in != nullptr)
+    return fail(VM_EINVAL, "precomputed activations need an output");
+  if (!aligned16(a->x) || (a->activation_in && !aligned16(a->activation_in)))
+    return fail(VM_EINVAL, "activations must be 16-byte aligned");
+  if ((a->shared == nullptr) != (a->shared_gate == nullptr))
+    return fail(VM_EINVAL, "shared and shared_gate must be provided together");
+  if (a->shared_y != nullptr && a->shared != nullptr)
+    return fail(VM_EINVAL, "provide shared_y or shared parts, not both");
+  if (a->scores == nullptr && (a->shared_y != nullptr || a->shared != nullptr))
+    return fail(VM_EINVAL, "a shared term needs scores");
+  if (!proj_ok(a->gate) || !proj_ok(a->up) || !proj_ok(a->down))
+    return fail(VM_EINVAL, "projection weight, scales and biases must be given together (weights 16-byte aligned)");
+  if (a->pool.base == nullptr && a->gate.weight == nullptr && a->stream.base == nullptr)
+    return fail(VM_EINVAL, "neither dense projections nor a pool view was given");
+  if (a->slot_table != nullptr && a->pool.base == nullptr)
+    return fail(VM_EINVAL, "a slot table needs a pool view");
+  if (a->stream.base != nullptr && a->pool.base == nullptr)
+    return fail(VM_EINVAL, "stream pack requires a resident slab pack");
+  int rc = check_pool(a->pool, H, I);
+  if (rc != VM_OK) return rc;
+  rc = check_pool(a->stream, H, I);
+  if (rc != VM_OK) return rc;
+  if (!vm::gateup_supported(H)) return fail(VM_EUNSUPPORTED, "hidden_size %u is above the decode kernel bound", H);
+  if (!vm::down_supported(I, K, a->act_dtype))
+    return fail(VM_EUNSUPPORTED, "inter_size %u with %u slots is above the decode kernel bound", I, K);
+
+  const uint64_t need = vm_moe_execute_workspace(T, K, I, a->act_dtype);
+  void* act = const_cast<void*>(a->activation_in);
+  if (act == nullptr) {
+    act = a->activation_out;
+    if (act == nullptr) {
+      if (a->workspace == nullptr || a->workspace_bytes < need)
+        return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)need);
+      act = a->workspace;
+    }
+    vm::GateUpLaunch g{};
+    g.x = a->x;
+    g.routes = a->routes;
+    g.slot_table = a->slot_table;
+    g.gate = to_ptrs(a->gate);
+    g.up = to_ptrs(a->up);
+    g.pool = to_pool(a->pool);
+    g.stream = to_pool(a->stream);
+    g.act = act;
+    g.gate_out = a->gate_out;
+    g.up_out = a->up_out;
+    g.status = a->status;
+    g.tokens = T;
+    g.slots = K;
+    g.hidden = H;
+    g.inter = I;
+    g.experts = a->expert_count;
+    g.has_shared = 0;
+    g.act_dtype = static_cast<int>(a->act_dtype);
+    hipError_t e = vm::launch_gateup(g, stream);
+    if (e != hipSuccess) return hip_fail(e, "gate/up launch");
+  }
+  if (a->output == nullptr) return VM_OK;
+  vm::DownLaunch d{};
+  d.act = act;
+  d.routes = a->routes;
+  d.slot_table = a->slot_table;
+  d.down = to_ptrs(a->down);
+  d.pool = to_pool(a->pool);
+  d.stream = to_pool(a->stream);
+  d.scores = a->scores;
+  d.score_dtype = static_cast<int>(a->score_dtype);
+  d.shared_y = a->shared_y;
+  d.shared = a->shared;
+  d.shared_gate = a->shared_gate;
+  d.out = a->output;
+  d.status = a->status;
+  d.tokens = T;
+  d.slots = K;
+  d.hidden = H;
+  d.inter = I;
+  d.experts = a->expert_count;
+  d.has_shared = 0;
+  d.act_dtype = static_cast<int>(a->act_dtype);
+  hipError_t e = vm::launch_down(d, stream);
+  if (e != hipSuccess) return hip_fail(e, "down launch");
+  return VM_OK;
+}
+
+// ------------------------------------------------------------- router ---
+
+uint64_t vm_router_workspace(uint32_t tokens, uint32_t expert_count) {
+  return kAlign + align_up(uint64_t(tokens) * expert_count * 4);
+}
+
+static int validate_router(uint32_t T, uint32_t H, uint32_t E, uint32_t K, uint32_t dtype) {
+  if (dtype > VM_F32) return fail(VM_EINVAL, "unknown dtype");
+  if (T == 0) return fail(VM_EINVAL, "tokens must be positive");
+  if (E == 0 || E > kMaxExperts) return fail(VM_EINVAL, "expert_count must be in 1..%u", kMaxExperts);
+  if (K == 0 || K > kMaxTopK) return fail(VM_EINVAL, "top_k must be in 1..%u", kMaxTopK);
+  if (K > E) return fail(VM_EINVAL, "top_k cannot exceed expert_count");
+  if (H == 0 || H % 32) return fail(VM_EINVAL, "hidden_size must be a positive multiple of 32");
+  if (H > 8192) return fail(VM_EUNSUPPORTED, "hidden_size %u is above the router kernel bound (8192)", H);
+  return VM_OK;
+}
+
+int vm_router_topk(const VmRouterArgs* a, void* stream_ptr) {
+  if (a == nullptr) return fail(VM_EINVAL, "null arguments");
+  int rc = validate_router(a->tokens, a->hidden_size, a->expert_count, a->top_k, a->act_dtype);
+  if (rc != VM_OK) return rc;
+  if (a->x == nullptr || a->weight == nullptr || a->inds == nullptr || a->scores == nullptr)
+    return fail(VM_EINVAL, "x, weight, inds and scores are required");
+  if (!aligned16(a->x) || !aligned16(a->weight)) return fail(VM_EINVAL, "x and weight must be 16-byte aligned");
+  const uint64_t need = vm_router_workspace(a->tokens, a->expert_count);
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)need);
+  vm::RouterLaunch r{};
+  r.x = a->x;
+  r.weight = a->weight;
+  r.bias = a->logit_bias;
+  r.inds = a->inds;
+  r.scores = a->scores;
+  r.gates = a->gates;
+  r.counter = static_cast<uint32_t*>(a->workspace);
+  r.logits = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + kAlign);
+  r.tokens = a->tokens;
+  r.hidden = a->hidden_size;
+  r.experts = a->expert_count;
+  r.top_k = a->top_k;
+  r.act_dtype = static_cast<int>(a->act_dtype);
+  r.blend = a->renorm_blend;
+  hipError_t e = vm::launch_router(r, static_cast<hipStream_t>(stream_ptr));
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  return VM_OK;
+}
+
+// -------------------------------------------------------------- layer ---
+// workspace: [counter | pad] [logits T*E f32] [act T*S*I] [sig T] [inds T*K] [scores T*K]
+
+struct LayerWs {
+  uint64_t logits, act, sig, inds, scores, total;
+};
+
+static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_t E, uint32_t dtype) {
+  LayerWs w{};
+  const uint32_t S = K + (Is ? 1 : 0);
+  w.logits = kAlign;
+  w.act = w.logits + align_up(uint64_t(T) * E * 4);
+  w.sig = w.act + align_up(uint64_t(T) * S * I * act_bytes(dtype));
+  w.inds = w.sig + align_up(uint64_t(T) * act_bytes(dtype));
+  w.scores = w.inds + align_up(uint64_t(T) * K * 4);
+  w.total = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
+  return w;
+}
+
+uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t inter_size, uint32_t shared_inter,
+                                uint32_t expert_count, uint32_t act_dtype) {
+  return layer_ws(tokens, top_k, inter_size, shared_inter, expert_count, act_dtype).total;
+}
+
+int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
+  if (a == nullptr) return fail(VM_EINVAL, "null arguments");
+  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
+  int rc = validate_router(T, H, E, K, a->act_dtype);
+  if (rc != VM_OK) return rc;
+  if (T > VM_LAYER_MAX_TOKENS) return fail(VM_EINVAL, "tokens must be in 1..%u", VM_LAYER_MAX_TOKENS);
+  if (a->group_size != 32) return fail(VM_EUNSUPPORTED, "group_size must be 32");
+  if (I == 0 || I % 32) return fail(VM_EINVAL, "Q4/G32 projection inputs must be group aligned");
+  if (a->shared_inter != 0 && a->shared_inter != I)
+    return fail(VM_EUNSUPPORTED, "shared_inter must be 0 or equal to inter_size");
+  if (a->x == nullptr || a->output == nullptr || a->router_weight == nullptr)
+    return fail(VM_EINVAL, "x, output and router_weight are required");
+  if (!aligned16(a->x) || !aligned16(a->router_weight)) return fail(VM_EINVAL, "x and router weight must be 16-byte aligned");
+  if (a->slot_table != nullptr && a->pool.base == nullptr) return fail(VM_EINVAL, "a slot table needs a pool view");
+  if (a->slot_table == nullptr && a->gate.weight == nullptr)
+    return fail(VM_EINVAL, "routed experts need a slot table with a pool view, or dense projections");
+  if (!proj_ok(a->gate) || !proj_ok(a->up) || !proj_ok(a->down)) return fail(VM_EINVAL, "malformed routed projection");
+  const bool shared = a->shared_inter != 0;
+  if (shared) {
+    if (a->shared_gate_proj.weight == nullptr || a->shared_up_proj.weight == nullptr ||
+        a->shared_down_proj.weight == nullptr || a->shared_expert_gate.weight == nullptr)
+      return fail(VM_EINVAL, "shared expert projections and its gate are required when shared_inter > 0");
+    if (!proj_ok(a->shared_gate_proj) || !proj_ok(a->shared_up_proj) || !proj_ok(a->shared_down_proj) ||
+        !proj_ok(a->shared_expert_gate))
+      return fail(VM_EINVAL, "malformed shared projection");
+  }
+  rc = check_pool(a->pool, H, I);
+  if (rc != VM_OK) return rc;
+  const uint32_t S = K + (shared ? 1 : 0);
+  if (!vm::gateup_supported(H)) return fail(VM_EUNSUPPORTED, "hidden_size %u is above the decode kernel bound", H);
+  if (!vm::down_supported(I, S, a->act_dtype)) return fail(VM_EUNSUPPORTED, "inter_size %u is above the decode kernel bound", I);
+  const LayerWs w = layer_ws(T, K, I, a->shared_inter, E, a->act_dtype);
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
+  char* ws = static_cast<char*>(a->workspace);
+  int32_t* inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
+  void* scores = a->scores_out != nullptr ? a->scores_out : static_cast<void*>(ws + w.scores);
+  const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
+  if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  hipError_t e = hipSuccess;
+
+  if (phases & VM_PHASE_ROUTER) {
+    vm::RouterLaunch r{};
+    r.x = a->x;
+    r.weight = a->router_weight;
+    r.bias = a->router_bias;
+    r.inds = inds;
+    r.scores = scores;
+    r.counter = reinterpret_cast<uint32_t*>(ws);
+    r.logits = reinterpret_cast<float*>(ws + w.logits);
+    if (shared) r.seg = to_ptrs(a->shared_expert_gate);
+    r.shared_sig = ws + w.sig;
+    r.tokens = T;
+    r.hidden = H;
+    r.experts = E;
+    r.top_k = K;
+    r.act_dtype = static_cast<int>(a->act_dtype);
+    r.blend = a->renorm_blend;
+    e = vm::launch_router(r, stream);
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+  }
+  if (!(phases & VM_PHASE_EXPERTS)) return VM_OK;
+
+  vm::GateUpLaunch g{};
+  g.x = a->x;
+  g.routes = reinterpret_cast<const uint32_t*>(inds);
+  g.slot_table = a->slot_table;
+  g.gate = to_ptrs(a->gate);
+  g.up = to_ptrs(a->up);
+  if (shared) {
+    g.shared_gate = to_ptrs(a->shared_gate_proj);
+    g.shared_up = to_ptrs(a->shared_up_proj);
+  }
+  g.pool = to_pool(a->pool);
+  g.act = ws + w.act;
+  g.status = a->status;
+  g.tokens = T;
+  g.slots = K;
+  g.hidden = H;
+  g.inter = I;
+  g.experts = E;
+  g.has_shared = shared ? 1 : 0;
+  g.act_dtype = static_cast<int>(a->act_dtype);
+  e = vm::launch_gateup(g, stream);
+  if (e != hipSuccess) return hip_fail(e, "gate/up launch");
+
+  vm::DownLaunch d{};
+  d.act = ws + w.act;
+  d.routes = reinterpret_cast<const uint32_t*>(inds);
+  d.slot_table = a->slot_table;
+  d.down = to_ptrs(a->down);
+  if (shared) d.shared_down = to_ptrs(a->shared_down_proj);
+  d.shared_sig = ws + w.sig;
+  d.pool = to_pool(a->pool);
+  d.scores = scores;
+  d.score_dtype = static_cast<int>(a->act_dtype);
+  d.out = a->output;
+  d.status = a->status;
+  d.tokens = T;
+  d.slots = K;
+  d.hidden = H;
+  d.inter = I;
+  d.experts = E;
+  d.has_shared = shared ? 1 : 0;
+  d.act_dtype = static_cast<int>(a->act_dtype);
+  e = vm::launch_down(d, stream);
+  if (e != hipSuccess) return hip_fail(e, "down launch");
+  return VM_OK;
+}
+
+// ------------------------------------------------------------ combine ---
+
+int vm_weighted_combine(const void* expert_outputs, const void* scores, void* out, uint32_t tokens, uint32_t slots,
+                        uint32_t hidden_size, uint32_t act_dtype, uint32_t score_dtype, void* stream) {
+  if (expert_outputs == nullptr || scores == nullptr || out == nullptr) return fail(VM_EINVAL, "null pointer");
+  if (act_dtype > VM_F32 || score_dtype > VM_F32) return fail(VM_EINVAL, "unknown dtype");
+  if (tokens == 0 || slots == 0 || hidden_size == 0) return fail(VM_EINVAL, "empty combine");
+  hipError_t e = vm::launch_weighted_combine(expert_outputs, scores, out, tokens, slots, hidden_size,
+                                             static_cast<int>(act_dtype), static_cast<int>(score_dtype),
+                                             static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return VM_OK;
+}
+
+// -------------------------------------------------------------- stage ---
+
+int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride, uint64_t pool_records,
+                  const void* src_host, uint64_t src_stride, uint64_t src_records, uint64_t record_bytes,
+                  const int64_t* src_index, const int64_t* dst_slot, uint32_t count, void* stream) {
+  if (count == 0) return VM_OK;
+  if (pool_base == nullptr || src_host == nullptr || src_index == nullptr || dst_slot == nullptr)
+    return fail(VM_EINVAL, "null pointer");
+  if (record_bytes == 0 || record_bytes > record_stride || record_bytes > src_stride)
+    return fail(VM_EINVAL, "record_bytes must be in 1..min(record_stride, src_stride)");
+  for (uint32_t i = 0; i < count; ++i) {
+    if (src_index[i] < 0 || uint64_t(src_index[i]) >= src_records)
+      return fail(VM_EINVAL, "src_index[%u] = %lld is outside 0..%llu", i, (long long)src_index[i],
+                  (unsigned long long)src_records);
+    if (dst_slot[i] < 0 || uint64_t(dst_slot[i]) >= pool_records)
+      return fail(VM_EINVAL, "dst_slot[%u] = %lld is outside 0..%llu", i, (long long)dst_slot[i],
+                  (unsigned long long)pool_records);
+  }
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  uint32_t i = 0;
+  while (i < count) {
+    uint32_t j = i + 1;
+    // merge runs that are consecutive on both sides when the strides agree
+    while (j < count && record_bytes == record_stride && record_stride == src_stride &&
+           src_index[j] == src_index[i] + (j - i) && dst_slot[j] == dst_slot[i] + (j - i))
+      ++j;
+    const uint64_t bytes = (j - i - 1) * record_stride + record_bytes;
+    char* dst = static_cast<char*>(pool_base) + header_size + uint64_t(dst_slot[i]) * record_stride;
+    const char* src = static_cast<const char*>(src_host) + uint64_t(src_index[i]) * src_stride;
+    hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync");
+    i = j;
+  }
+  return VM_OK;
+}
+
+// ------------------------------------------------------------- timing ---
+
+int vm_timing_enable(int enabled) {
+  Timing& t = timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  t.enabled = enabled != 0;
+  return VM_OK;
+}
+
+int vm_timing_read(const char* name, double* total_ms, uint64_t* launches) {
+  if (name == nullptr || total_ms == nullptr || launches == nullptr) return fail(VM_EINVAL, "null pointer");
+  Timing& t = timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  int rc = drain_timing(t);
+  if (rc != VM_OK) return rc;
+  auto it = t.totals.find(name);
+  *total_ms = it == t.totals.end() ? 0.0 : it->second.first;
+  *launches = it == t.totals.end() ? 0 : it->second.second;
+  return VM_OK;
+}
+
+int vm_timing_reset(void) {
+  Timing& t = timing();
+  std::lock_guard<std::mutex> lock(t.mu);
+  int rc = drain_timing(t);
+  t.totals.clear();
+  return rc;
+}
+
+// The grouped (prefill / batched) path lives in grouped.hip.
+
+}  // extern "C"

@@ -1,0 +1,257 @@
+"""HBM-resident expert pool with an LRU slot table.
+
+Counterpart of the reference's ``ExpertPool`` (models/flashnext/expert_pool.py:78-294):
+
+* one device allocation: a 4 KiB header, then fixed-stride expert records
+  (``veymoe.layout.RecordLayout``), addressed by the kernels through route
+  words ``SLOT_BIT | slot`` or through a per-layer int32 slot table
+  (expert -> slot, -1 = absent) that the kernels read on the device;
+* ``assign`` has the reference's LRU semantics exactly (expert_pool.py:123-159):
+  distinct experts in first-seen order, hits move to the most recent end and
+  are counted once per distinct expert, misses take the lowest free slot or
+  evict the least recently used key, and a distinct set larger than the pool is
+  refused before any state changes;
+* misses are filled from pinned host memory (``HostRecordStore``, standing in
+  for the SSD reads of ``fill``/``_fill_part``, :201-220, :258-287) with
+  ``hipMemcpyAsync`` on a side stream (``vm_pool_stage``); an event joins the
+  compute stream, and the copy stream first waits for the compute stream so a
+  slot is overwritten only after its last reader (:19-22);
+* a failed fill invalidates its misses so no partial record becomes a hit
+  (``invalidate``, :222-231).
+"""
+from __future__ import annotations
+
+import ctypes
+from collections import OrderedDict
+from typing import Iterable
+
+import numpy as np
+import torch
+
+from . import _lib
+from .device import stream_handle
+from .layout import HEADER, PARTS, SLOT_BIT, RecordLayout
+
+
+class HostRecordStore:
+    """Expert records in pinned host memory, keyed by (layer, expert)."""
+
+    def __init__(self, layout: RecordLayout, capacity: int, pin: bool = True):
+        self.layout = layout
+        self.capacity = int(capacity)
+        self.buffer = torch.empty((self.capacity, layout.record_stride), dtype=torch.uint8, pin_memory=pin)
+        self._row_of = {}
+
+    def __contains__(self, key):
+        return key in self._row_of
+
+    def put(self, layer: int, expert: int, record: np.ndarray) -> int:
+        key = (int(layer), int(expert))
+        row = self._row_of.get(key)
+        if row is None:
+            row = len(self._row_of)
+            if row >= self.capacity:
+                raise ValueError("host record store is full")
+            self._row_of[key] = row
+        self.buffer[row].numpy()[: record.size] = record
+        return row
+
+    def alias(self, layer: int, expert: int, row: int) -> None:
+        """Map (layer, expert) to an existing row (records shared between ids)."""
+        if not 0 <= row < self.capacity:
+            raise ValueError("row outside the store")
+        self._row_of[(int(layer), int(expert))] = int(row)
+
+    def row(self, layer: int, expert: int) -> int:
+        return self._row_of[(int(layer), int(expert))]
+
+
+class ExpertPool:
+    def __init__(self, layout: RecordLayout, slots: int, *, layers: int = 1, experts: int = 512,
+                 device=None, header_size: int = HEADER):
+        if slots < 16:
+            raise ValueError("expert pool is too small for one decode layer")
+        self.layout = layout
+        self.slots = int(slots)
+        self.layers = int(layers)
+        self.experts = int(experts)
+        self.header_size = int(header_size)
+        self.stride = layout.record_stride
+        self.device = torch.device("cuda") if device is None else torch.device(device)
+        self.buffer = torch.zeros(self.header_size + self.slots * self.stride, dtype=torch.uint8,
+                                  device=self.device)
+        self.slot_table = torch.full((self.layers, self.experts), -1, dtype=torch.int32, device=self.device)
+        self._host_table = np.full((self.layers, self.experts), -1, dtype=np.int32)
+        self._dirty = set()
+        self._slot_of: "OrderedDict[tuple, int]" = OrderedDict()
+        self._free = list(range(self.slots - 1, -1, -1))
+        self.hits = 0
+        self.misses = 0
+        self.bytes_staged = 0
+        self._copy_stream = None
+
+    @classmethod
+    def from_bytes(cls, layout: RecordLayout, size_bytes: int, **kwargs):
+        """Size the pool like the reference: (bytes - header) // stride slots (expert_pool.py:92)."""
+        header = kwargs.get("header_size", HEADER)
+        return cls(layout, (int(size_bytes) - header) // layout.record_stride, **kwargs)
+
+    # ------------------------------------------------------------ LRU ---
+    @property
+    def usable_slots(self) -> int:
+        return len(self._free) + len(self._slot_of)
+
+    def _map(self, key, slot):
+        layer, expert = key
+        self._host_table[layer, expert] = slot
+        self._dirty.add(layer)
+
+    def _unmap(self, key):
+        layer, expert = key
+        self._host_table[layer, expert] = -1
+        self._dirty.add(layer)
+
+    def assign(self, layer: int, experts: Iterable[int] | int):
+        """Assign a distinct expert set that fits in the pool, or fail before mutation."""
+        if isinstance(experts, (int, np.integer)):
+            experts = [int(experts)]
+        distinct = list(dict.fromkeys(int(e) for e in experts))
+        if len(distinct) > self.usable_slots:
+            raise ValueError("requested experts exceed expert pool capacity")
+        slot_of = self._slot_of
+        slots, misses = {}, []
+        for expert in distinct:
+            slot = slot_of.get((layer, expert))
+            if slot is not None:
+                slot_of.move_to_end((layer, expert))
+                slots[expert] = slot
+        self.hits += len(slots)
+        for expert in distinct:
+            if expert in slots:
+                continue
+            if self._free:
+                slot = self._free.pop()
+            else:
+                old, slot = slot_of.popitem(last=False)
+                self._unmap(old)
+            slot_of[(layer, expert)] = slot
+            self._map((layer, expert), slot)
+            slots[expert] = slot
+            misses.append((expert, slot))
+        self.misses += len(misses)
+        return slots, misses
+
+    def invalidate(self, layer: int, misses) -> None:
+        """Return the slots of failed fills to the free list, never as hits."""
+        for expert, slot in misses:
+            key = (layer, expert)
+            if self._slot_of.get(key) == slot:
+                self._free.append(self.discard_slot(key))
+
+    def discard_slot(self, key):
+        slot = self._slot_of.pop(key)
+        self._unmap(key)
+        return slot
+
+    def resident(self, layer: int, expert: int) -> bool:
+        return (layer, expert) in self._slot_of
+
+    # ---------------------------------------------------------- device ---
+    def view(self) -> _lib.VmPoolView:
+        view = _lib.VmPoolView()
+        view.base = self.buffer.data_ptr()
+        view.header_size = self.header_size
+        view.record_stride = self.stride
+        for i, offset in enumerate(self.layout.part_offsets()):
+            view.part_offset[i] = offset
+        view.records = self.slots
+        return view
+
+    def table(self, layer: int) -> torch.Tensor:
+        return self.slot_table[layer]
+
+    def sync_tables(self) -> None:
+        """Upload the slot-table rows changed since the last call (ordered on the
+        current stream before any kernel launched after it)."""
+        for layer in sorted(self._dirty):
+            row = torch.from_numpy(self._host_table[layer].copy())
+            self.slot_table[layer].copy_(row, non_blocking=False)
+        self._dirty.clear()
+
+    def place(self, layer: int, expert: int, slot: int) -> None:
+        """Pin (layer, expert) to ``slot`` directly (resident setups); the slot
+        must be free."""
+        key = (int(layer), int(expert))
+        if key in self._slot_of:
+            raise ValueError(f"{key} is already resident")
+        try:
+            self._free.remove(int(slot))
+        except ValueError:
+            raise ValueError(f"slot {slot} is not free") from None
+        self._slot_of[key] = int(slot)
+        self._map(key, int(slot))
+
+    def place_all(self, layer: int, slots) -> None:
+        """Pin expert e of ``layer`` to ``slots[e]`` for every e (resident setups)."""
+        slots = [int(s) for s in slots]
+        taken = set(slots)
+        if len(taken) != len(slots) or not taken.issubset(self._free):
+            raise ValueError("slots must be distinct and free")
+        for expert, slot in enumerate(slots):
+            key = (int(layer), expert)
+            if key in self._slot_of:
+                raise ValueError(f"{key} is already resident")
+            self._slot_of[key] = slot
+            self._map(key, slot)
+        self._free = [s for s in self._free if s not in taken]
+
+    def record(self, slot: int) -> torch.Tensor:
+        """Device bytes of one record (a view)."""
+        start = self.header_size + int(slot) * self.stride
+        return self.buffer[start:start + self.stride]
+
+    def copy_stream(self):
+        if self._copy_stream is None:
+            self._copy_stream = torch.cuda.Stream(device=self.device)
+        return self._copy_stream
+
+    def stage(self, source: HostRecordStore, layer: int, misses, compute_stream=None) -> torch.cuda.Event | None:
+        """Copy the records of ``misses`` [(expert, slot)] from pinned host memory
+        into their slots on the side stream; the compute stream waits for it."""
+        if not misses:
+            return None
+        order = sorted(misses, key=lambda item: item[1])
+        src = (ctypes.c_int64 * len(order))(*[source.row(layer, e) for e, _ in order])
+        dst = (ctypes.c_int64 * len(order))(*[slot for _, slot in order])
+        compute = torch.cuda.current_stream(self.device) if compute_stream is None else compute_stream
+        copier = self.copy_stream()
+        # a slot may still be read by kernels queued before this point
+        copier.wait_stream(compute)
+        rc = _lib.lib().vm_pool_stage(
+            self.buffer.data_ptr(), self.header_size, self.stride, self.slots,
+            source.buffer.data_ptr(), source.layout.record_stride, source.capacity,
+            self.layout.record_bytes, src, dst, len(order), stream_handle(copier))
+        if rc != _lib.VM_OK:
+            self.invalidate(layer, misses)
+            _lib.check(rc)
+        event = torch.cuda.Event()
+        event.record(copier)
+        compute.wait_event(event)
+        self.bytes_staged += len(order) * self.layout.record_bytes
+        return event
+
+    def fill(self, layer: int, misses, source: HostRecordStore, compute_stream=None):
+        """Stage misses; on any failure invalidate them before re-raising."""
+        try:
+            return self.stage(source, layer, misses, compute_stream)
+        except BaseException:
+            self.invalidate(layer, misses)
+            raise
+
+
+def route_words(slots_of: dict, routed) -> np.ndarray:
+    """``SLOT_BIT | slot`` for every routed expert (expert_cache.py:1915-1917)."""
+    return np.array([SLOT_BIT | slots_of[int(e)] for e in routed], dtype=np.uint32)
+
+
+__all__ = ["ExpertPool", "HostRecordStore", "PARTS", "SLOT_BIT", "route_words"]
