@@ -262,6 +262,14 @@ int vm_timing_enable(int enabled);
 int vm_timing_read(const char* name, double* total_ms, uint64_t* launches);
 int vm_timing_reset(void);
 
+/* Phase trace (diagnostics): while a device buffer is set, the decode
+ * kernels write 100 MHz timestamps (s_memrealtime) of their phases, one
+ * record of 16 uint64 per block: [kernel id, block, t0 .. t11, 0, 0]; the
+ * records of one launch are consecutive, in block order.  Pass NULL to stop.
+ * vm_trace_records returns the number of records reserved since the set. */
+int vm_trace_set(void* device_buffer, uint64_t bytes);
+uint64_t vm_trace_records(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -322,31 +322,39 @@ int vm_router_topk(const VmRouterArgs* a, void* stream_ptr) {
   const uint64_t need = vm_router_workspace(a->tokens, a->expert_count);
   if (a->workspace == nullptr || a->workspace_bytes < need)
     return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)need);
-  vm::RouterLaunch r{};
-  r.x = a->x;
-  r.weight = a->weight;
-  r.bias = a->logit_bias;
-  r.inds = a->inds;
-  r.scores = a->scores;
-  r.gates = a->gates;
-  r.counter = static_cast<uint32_t*>(a->workspace);
-  r.logits = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + kAlign);
-  r.tokens = a->tokens;
-  r.hidden = a->hidden_size;
-  r.experts = a->expert_count;
-  r.top_k = a->top_k;
-  r.act_dtype = static_cast<int>(a->act_dtype);
-  r.blend = a->renorm_blend;
-  hipError_t e = vm::launch_router(r, static_cast<hipStream_t>(stream_ptr));
+  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  float* logits = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + kAlign);
+  vm::FrontLaunch f{};
+  f.x = a->x;
+  f.weight = a->weight;
+  f.bias = a->logit_bias;
+  f.logits = logits;
+  f.tokens = a->tokens;
+  f.hidden = a->hidden_size;
+  f.experts = a->expert_count;
+  f.act_dtype = static_cast<int>(a->act_dtype);
+  hipError_t e = vm::launch_front(f, stream);
   if (e != hipSuccess) return hip_fail(e, "router launch");
+  vm::SelectLaunch s{};
+  s.logits = logits;
+  s.inds = a->inds;
+  s.scores = a->scores;
+  s.gates = a->gates;
+  s.tokens = a->tokens;
+  s.experts = a->expert_count;
+  s.top_k = a->top_k;
+  s.act_dtype = static_cast<int>(a->act_dtype);
+  s.blend = a->renorm_blend;
+  e = vm::launch_select(s, stream);
+  if (e != hipSuccess) return hip_fail(e, "select launch");
   return VM_OK;
 }
 
 // -------------------------------------------------------------- layer ---
-// workspace: [counter | pad] [logits T*E f32] [act T*S*I] [sig T] [inds T*K] [scores T*K]
+// workspace: [reserved] [logits T*E f32] [act T*S*I] [sig T] [inds T*K] [scores T*K] [words T*K]
 
 struct LayerWs {
-  uint64_t logits, act, sig, inds, scores, total;
+  uint64_t logits, act, sig, inds, scores, words, total;
 };
 
 static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_t E, uint32_t dtype) {
@@ -357,7 +365,8 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   w.sig = w.act + align_up(uint64_t(T) * S * I * act_bytes(dtype));
   w.inds = w.sig + align_up(uint64_t(T) * act_bytes(dtype));
   w.scores = w.inds + align_up(uint64_t(T) * K * 4);
-  w.total = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
+  w.words = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
+  w.total = w.words + align_up(uint64_t(T) * K * 4);
   return w;
 }
 
@@ -404,35 +413,49 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   char* ws = static_cast<char*>(a->workspace);
   int32_t* inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
   void* scores = a->scores_out != nullptr ? a->scores_out : static_cast<void*>(ws + w.scores);
+  uint32_t* words = reinterpret_cast<uint32_t*>(ws + w.words);
+  float* logits = reinterpret_cast<float*>(ws + w.logits);
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  // fused: the gate/up blocks select the experts themselves from the logits;
+  // split: a select kernel publishes inds/scores for the host between phases
+  const bool fused = phases == (VM_PHASE_ROUTER | VM_PHASE_EXPERTS);
   hipError_t e = hipSuccess;
 
   if (phases & VM_PHASE_ROUTER) {
-    vm::RouterLaunch r{};
-    r.x = a->x;
-    r.weight = a->router_weight;
-    r.bias = a->router_bias;
-    r.inds = inds;
-    r.scores = scores;
-    r.counter = reinterpret_cast<uint32_t*>(ws);
-    r.logits = reinterpret_cast<float*>(ws + w.logits);
-    if (shared) r.seg = to_ptrs(a->shared_expert_gate);
-    r.shared_sig = ws + w.sig;
-    r.tokens = T;
-    r.hidden = H;
-    r.experts = E;
-    r.top_k = K;
-    r.act_dtype = static_cast<int>(a->act_dtype);
-    r.blend = a->renorm_blend;
-    e = vm::launch_router(r, stream);
+    vm::FrontLaunch f{};
+    f.x = a->x;
+    f.weight = a->router_weight;
+    f.bias = a->router_bias;
+    f.logits = logits;
+    if (shared) f.seg = to_ptrs(a->shared_expert_gate);
+    f.shared_sig = ws + w.sig;
+    f.tokens = T;
+    f.hidden = H;
+    f.experts = E;
+    f.act_dtype = static_cast<int>(a->act_dtype);
+    e = vm::launch_front(f, stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");
+    if (!fused) {
+      vm::SelectLaunch s{};
+      s.logits = logits;
+      s.inds = inds;
+      s.scores = scores;
+      s.tokens = T;
+      s.experts = E;
+      s.top_k = K;
+      s.act_dtype = static_cast<int>(a->act_dtype);
+      s.blend = a->renorm_blend;
+      e = vm::launch_select(s, stream);
+      if (e != hipSuccess) return hip_fail(e, "select launch");
+    }
   }
   if (!(phases & VM_PHASE_EXPERTS)) return VM_OK;
 
   vm::GateUpLaunch g{};
   g.x = a->x;
   g.routes = reinterpret_cast<const uint32_t*>(inds);
+  g.logits = fused ? logits : nullptr;
   g.slot_table = a->slot_table;
   g.gate = to_ptrs(a->gate);
   g.up = to_ptrs(a->up);
@@ -442,6 +465,9 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   }
   g.pool = to_pool(a->pool);
   g.act = ws + w.act;
+  g.inds_out = fused ? inds : nullptr;
+  g.scores_out = fused ? scores : nullptr;
+  g.words_out = fused ? words : nullptr;
   g.status = a->status;
   g.tokens = T;
   g.slots = K;
@@ -450,13 +476,14 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   g.experts = E;
   g.has_shared = shared ? 1 : 0;
   g.act_dtype = static_cast<int>(a->act_dtype);
+  g.blend = a->renorm_blend;
   e = vm::launch_gateup(g, stream);
   if (e != hipSuccess) return hip_fail(e, "gate/up launch");
 
   vm::DownLaunch d{};
   d.act = ws + w.act;
-  d.routes = reinterpret_cast<const uint32_t*>(inds);
-  d.slot_table = a->slot_table;
+  d.routes = fused ? words : reinterpret_cast<const uint32_t*>(inds);
+  d.slot_table = fused ? nullptr : a->slot_table;
   d.down = to_ptrs(a->down);
   if (shared) d.shared_down = to_ptrs(a->shared_down_proj);
   d.shared_sig = ws + w.sig;
@@ -476,6 +503,7 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   if (e != hipSuccess) return hip_fail(e, "down launch");
   return VM_OK;
 }
+
 
 // ------------------------------------------------------------ combine ---
 
@@ -555,6 +583,44 @@ int vm_timing_reset(void) {
   t.totals.clear();
   return rc;
 }
+
+// ------------------------------------------------------------- trace ----
+
+static struct {
+  std::mutex mu;
+  uint64_t* buf = nullptr;
+  uint64_t capacity = 0;  // records of 8 uint64
+  uint64_t used = 0;
+} g_trace;
+
+int vm_trace_set(void* device_buffer, uint64_t bytes) {
+  std::lock_guard<std::mutex> lock(g_trace.mu);
+  g_trace.buf = static_cast<uint64_t*>(device_buffer);
+  g_trace.capacity = device_buffer != nullptr ? bytes / (8 * vm::kTraceWords) : 0;
+  g_trace.used = 0;
+  return VM_OK;
+}
+
+uint64_t vm_trace_records(void) {
+  std::lock_guard<std::mutex> lock(g_trace.mu);
+  return g_trace.used;
+}
+
+}  // extern "C"
+
+namespace vm {
+
+uint64_t* trace_reserve(uint32_t blocks) {
+  std::lock_guard<std::mutex> lock(g_trace.mu);
+  if (g_trace.buf == nullptr || g_trace.used + blocks > g_trace.capacity) return nullptr;
+  uint64_t* p = g_trace.buf + g_trace.used * kTraceWords;
+  g_trace.used += blocks;
+  return p;
+}
+
+}  // namespace vm
+
+extern "C" {
 
 // The grouped (prefill / batched) path lives in grouped.hip.
 

@@ -8,10 +8,41 @@
 
 namespace vm {
 
+// Route word written for a selected expert that has no pool slot: it is not
+// a slot word and is above every dense expert index, so resolution fails and
+// the status flag is raised.
+constexpr uint32_t kMissWord = 0x7fffffffu;
+
+// K1: router logits (and the shared expert's sigmoid gate).
+struct FrontLaunch {
+  const void* x;               // [T, H]
+  const uint16_t* weight;      // [E, H] bf16
+  const float* bias;           // optional [E]
+  float* logits;               // [T, E], rounded to the activation type
+  ProjPtrs seg;                // optional shared expert gate (H -> 1 Q4 row)
+  void* shared_sig;            // [T] activation dtype
+  uint64_t* trace;             // optional phase timestamps, 8 per block
+  uint32_t tokens, hidden, experts;
+  int act_dtype;
+};
+
+// Softmax / top-k / renormalisation of logits, one wave per token.
+struct SelectLaunch {
+  const float* logits;         // [T, E]
+  int32_t* inds;               // [T, K]
+  void* scores;                // [T, K] activation dtype
+  void* gates;                 // optional [T, E]
+  uint32_t tokens, experts, top_k;
+  int act_dtype;
+  float blend;
+};
+
+// K2: gate/up + SwiGLU of every (token, slot) pair and the shared pairs.
 struct GateUpLaunch {
   const void* x;               // [T, H]
-  const uint32_t* routes;      // [T, K] route words (or expert ids with slot_table)
-  const int32_t* slot_table;   // optional
+  const uint32_t* routes;      // [T, K] route words (or expert ids with slot_table) when logits == null
+  const float* logits;         // [T, E]: select the experts in the block prologue instead
+  const int32_t* slot_table;   // optional expert -> slot
   ProjPtrs gate, up;           // dense routed experts
   ProjPtrs shared_gate, shared_up;  // dense shared expert (pair j == K), optional
   PoolDev pool;
@@ -19,9 +50,14 @@ struct GateUpLaunch {
   void* act;                   // [T, S, I], S = K + has_shared
   void* gate_out;              // optional [T, K, I]
   void* up_out;                // optional [T, K, I]
+  int32_t* inds_out;           // logits path: [T, K] selected experts
+  void* scores_out;            // logits path: [T, K] renormalised scores
+  uint32_t* words_out;         // logits path: [T, K] resolved route words for the down kernel
   uint32_t* status;
+  uint64_t* trace;             // optional phase timestamps, 8 per block
   uint32_t tokens, slots, hidden, inter, experts, has_shared;
   int act_dtype;
+  float blend;
 };
 
 struct DownLaunch {
@@ -40,30 +76,15 @@ struct DownLaunch {
   const void* shared_gate;     // [T]
   void* out;
   uint32_t* status;
+  uint64_t* trace;             // optional phase timestamps, 8 per block
   uint32_t tokens, slots, hidden, inter, experts, has_shared;
   int act_dtype;
 };
 
-struct RouterLaunch {
-  const void* x;               // [T, H]
-  const uint16_t* weight;      // [E, H] bf16
-  const float* bias;           // optional [E]
-  int32_t* inds;               // [T, K]
-  void* scores;                // [T, K] activation dtype
-  void* gates;                 // optional [T, E]
-  float* logits;               // workspace [T, E]
-  uint32_t* counter;           // workspace, zero between launches
-  // optional shared expert gate (H -> 1 Q4 projection) computed by one extra block
-  ProjPtrs seg;
-  void* shared_sig;            // [T] activation dtype
-  uint32_t tokens, hidden, experts, top_k;
-  int act_dtype;
-  float blend;
-};
-
+hipError_t launch_front(const FrontLaunch& p, hipStream_t stream);
+hipError_t launch_select(const SelectLaunch& p, hipStream_t stream);
 hipError_t launch_gateup(const GateUpLaunch& p, hipStream_t stream);
 hipError_t launch_down(const DownLaunch& p, hipStream_t stream);
-hipError_t launch_router(const RouterLaunch& p, hipStream_t stream);
 hipError_t launch_weighted_combine(const void* values, const void* scores, void* out, uint32_t tokens,
                                    uint32_t slots, uint32_t hidden, int act_dtype, int score_dtype,
                                    hipStream_t stream);
@@ -72,8 +93,26 @@ hipError_t launch_weighted_combine(const void* values, const void* scores, void*
 bool gateup_supported(uint32_t hidden);
 bool down_supported(uint32_t inter, uint32_t slots_total, int act_dtype);
 
-// Kernel timing hooks (api.cpp).
+// Kernel timing hooks (api.hip).
 void timing_begin(const char* family, hipStream_t stream);
 void timing_end(const char* family, hipStream_t stream);
+// Phase-trace records for a launch of `blocks` blocks (null when tracing is off or full).
+uint64_t* trace_reserve(uint32_t blocks);
+
+// Phase timestamps: thread 0 of a block keeps them and writes one record of
+// 16 uint64: [kernel id, block, t0 .. t11, 0, 0].
+constexpr int kTraceWords = 16;
+constexpr int kTraceMarks = 12;
+struct PhaseTrace {
+  uint64_t t[kTraceMarks] = {};
+  __device__ __forceinline__ void mark(int i) { t[i] = __builtin_amdgcn_s_memrealtime(); }
+  __device__ __forceinline__ void write(uint64_t* trace, uint32_t kernel_id, uint32_t block) const {
+    uint64_t* r = trace + static_cast<size_t>(block) * kTraceWords;
+    r[0] = kernel_id;
+    r[1] = block;
+    for (int i = 0; i < kTraceMarks; ++i) r[2 + i] = t[i];
+    r[14] = r[15] = 0;
+  }
+};
 
 }  // namespace vm

@@ -153,6 +153,8 @@ SIGNATURES = {
     "vm_timing_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_uint64)]),
     "vm_timing_reset": (ctypes.c_int, []),
+    "vm_trace_set": (ctypes.c_int, [_vp, _c_u64]),
+    "vm_trace_records": (_c_u64, []),
 }
 
 
