@@ -13,8 +13,9 @@ Infinity Cache cannot serve repeated weights; inputs are resident in HBM.
 
 value = layer-tokens/s over the timed steps (graph replay of one pass over
 the layers per replay, unless --eager).  roofline: the gate/up kernel (the
-largest HBM consumer) timed with HIP events on its stream in a second pass
-over the same steps; bytes = algorithmic bytes of one launch.  cpu_baseline:
+largest HBM consumer) timed with HIP start/stop events attached to its own
+dispatches (hipExtLaunchKernelGGL) in a second, eager pass over the same
+steps; bytes = algorithmic bytes of one launch.  cpu_baseline:
 the C restatement of the same layer (oracle/cmoe.c, OpenMP) on a bounded
 sample of tokens, on this host's cores.
 """
@@ -201,7 +202,7 @@ def main():
         elapsed = time.perf_counter() - start
         ms_per_step = elapsed * 1e3 / steps
 
-        # roofline pass: same steps, eager, every kernel bracketed by HIP events on its stream
+        # roofline pass: same steps, eager, HIP events stamped by each kernel's own dispatch
         lib.vm_timing_reset()
         lib.vm_timing_enable(1)
         for _ in range(steps // layers):

@@ -94,8 +94,6 @@ struct Timing {
   std::map<std::string, std::vector<Pending>> pending;
   std::map<std::string, std::pair<double, uint64_t>> totals;
   std::vector<hipEvent_t> free_events;
-  // last begun event per family (launches are issued from one thread)
-  std::map<std::string, hipEvent_t> open;
 
   hipEvent_t get() {
     if (!free_events.empty()) {
@@ -137,27 +135,17 @@ int drain_timing(Timing& t) {
 
 namespace vm {
 
-void timing_begin(const char* family, hipStream_t stream) {
+bool timing_events(const char* family, hipEvent_t* start, hipEvent_t* stop) {
   Timing& t = timing();
-  if (!t.enabled) return;
+  if (!t.enabled) return false;
   std::lock_guard<std::mutex> lock(t.mu);
+  hipEvent_t s = t.get();
   hipEvent_t e = t.get();
-  if (e == nullptr) return;
-  hipEventRecord(e, stream);
-  t.open[family] = e;
-}
-
-void timing_end(const char* family, hipStream_t stream) {
-  Timing& t = timing();
-  if (!t.enabled) return;
-  std::lock_guard<std::mutex> lock(t.mu);
-  auto it = t.open.find(family);
-  if (it == t.open.end()) return;
-  hipEvent_t e = t.get();
-  if (e == nullptr) return;
-  hipEventRecord(e, stream);
-  t.pending[family].push_back({it->second, e});
-  t.open.erase(it);
+  if (s == nullptr || e == nullptr) return false;
+  t.pending[family].push_back({s, e});
+  *start = s;
+  *stop = e;
+  return true;
 }
 
 }  // namespace vm

@@ -1,26 +1,31 @@
 // Decode kernels of the routed-expert MoE layer for gfx950 (wave64).
 //
-// A decode layer is three launches with no in-kernel cross-block sync (a
-// device-scope fence costs more than a kernel boundary on this part):
+// A decode layer is three launches with no cross-block sync inside a kernel
+// (a device-scope release writes back the XCD's L2 and costs more than a
+// kernel boundary on this part):
 //
 //   k_front   router logits x . Wr^T (one row per wave, bf16 dot2) and the
 //             shared expert's H -> 1 Q4 gate with its sigmoid.
-//   k_gateup  every block of a routed pair first recomputes softmax + top-k
-//             of its token from the logits (identical in every block), maps
-//             the selected expert to its pool slot through an LDS copy of
-//             the slot table, then streams the gate and up Q4/G32 rows with
-//             SwiGLU in a block-parallel epilogue.  Shared-expert pairs skip
-//             the selection.  One block per token publishes indices, scores
-//             and route words for k_down.
+//   k_gateup  in every block of a routed pair, wave 0 recomputes the token's
+//             softmax from the logits and finds the expert of its slot's rank
+//             (ballot search + candidate ranking, no sort), maps it to its slot and
+//             hands the route word to the other waves through one barrier.
+//             Every lane then streams gate and up Q4/G32 rows against its
+//             activation groups held in registers; SwiGLU runs on the lanes
+//             that hold the row sums.  Shared-expert pairs skip the selection.
+//             One block per token publishes the ordered selection (indices,
+//             scores, route words) for k_down.
 //   k_down    down Q4/G32 GEMV of every slot of a token for a tile of output
-//             rows, then the router-score combine with the shared term.
+//             rows (wave w owns slots w, w+4, w+8), then the router-score
+//             combine with the shared term after one barrier.
 //   k_select  softmax + top-k alone (router entry point, split layer path).
 //
 // Bandwidth layout: one 16-byte load per lane covers one 32-input group of a
-// row (4 packed words); scale and bias are 2-byte loads that coalesce into one
-// 128-byte line per row; activations are staged once per block in LDS,
-// pre-paired for v_dot2 with the group sums alongside; row sums use DPP.
+// row (4 packed words); the scale and bias loads of 64 lanes coalesce into one
+// 128-byte line per row; activations are read by each lane for its own groups,
+// re-paired for v_dot2 with the group sums alongside; row sums use DPP.
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -35,72 +40,40 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
 constexpr int kMaxExpertsPerLane = 8;  // expert_count <= 512
-constexpr int kMaxTopK = 16;
 
 template <class A>
 constexpr bool is_bf16() {
   return std::is_same<A, ActBF16>::value;
 }
 
-// LDS words per 32-input group: bf16 16 pair words + sum + 128*sum (+2 pad);
-// f32 32 values + sum (+3 pad).  Strides of 20 / 36 words keep 16 lanes of
-// consecutive groups on distinct banks for 16-byte reads.
-template <class A>
-constexpr int lds_group_words() {
-  return is_bf16<A>() ? 20 : 36;
-}
-
-// Stage the 32 activations of group g (elements elem..elem+31) into LDS.
-template <class A>
-__device__ __forceinline__ void stage_group(const void* src, size_t elem, uint32_t* dst) {
-  if constexpr (is_bf16<A>()) {
-    const uint4* v = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + elem);
-    uint32_t raw[16], xp[16];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint4 r = v[q];
-      raw[4 * q + 0] = r.x; raw[4 * q + 1] = r.y; raw[4 * q + 2] = r.z; raw[4 * q + 3] = r.w;
-    }
-    pair_activations(raw, xp);
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-      reinterpret_cast<uint4*>(dst)[q] = make_uint4(xp[4 * q], xp[4 * q + 1], xp[4 * q + 2], xp[4 * q + 3]);
-    const float s = bf16_pair_sum(raw);
-    reinterpret_cast<uint2*>(dst)[8] = make_uint2(__float_as_uint(s), __float_as_uint(128.0f * s));
-  } else {
-    const float4* v = reinterpret_cast<const float4*>(static_cast<const float*>(src) + elem);
-    float s = 0.0f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const float4 r = v[q];
-      reinterpret_cast<float4*>(dst)[q] = r;
-      s += r.x + r.y + r.z + r.w;
-    }
-    dst[32] = __float_as_uint(s);
-  }
-}
-
-__device__ __forceinline__ void stage_zero(uint32_t* dst, int words) {
-  for (int i = 0; i < words; ++i) dst[i] = 0;
-}
-
-// One group's activations in registers, read back from LDS.
+// One 32-input activation group in registers.  fetch() issues the loads,
+// prepare() turns the raw values into the operands of the group dot.
 template <class A>
 struct GroupAct;
 
 template <>
 struct GroupAct<ActBF16> {
-  uint32_t xp[16];
+  uint32_t xp[16];  // after prepare(): pairs (x_{8i+n}, x_{8i+n+4}) at 4i+n
   float sum, sum128;
-  __device__ __forceinline__ void load_lds(const uint32_t* src) {
+  __device__ __forceinline__ void fetch(const void* src, size_t elem) {
+    const uint4* v = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(src) + elem);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const uint4 r = reinterpret_cast<const uint4*>(src)[q];
+      const uint4 r = v[q];
       xp[4 * q] = r.x; xp[4 * q + 1] = r.y; xp[4 * q + 2] = r.z; xp[4 * q + 3] = r.w;
     }
-    const uint2 s = reinterpret_cast<const uint2*>(src)[8];
-    sum = __uint_as_float(s.x);
-    sum128 = __uint_as_float(s.y);
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xp[i] = 0;
+  }
+  __device__ __forceinline__ void prepare() {
+    uint32_t raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) raw[i] = xp[i];
+    pair_activations(raw, xp);
+    sum = bf16_pair_sum(raw);
+    sum128 = 128.0f * sum;
   }
   // scale * sum(q x) + bias * sum(x); the dot carries +128*sum(x)
   __device__ __forceinline__ float apply(const uint4 w, float s, float b) const {
@@ -112,13 +85,23 @@ template <>
 struct GroupAct<ActF32> {
   float x[32];
   float sum;
-  __device__ __forceinline__ void load_lds(const uint32_t* src) {
+  __device__ __forceinline__ void fetch(const void* src, size_t elem) {
+    const float4* v = reinterpret_cast<const float4*>(static_cast<const float*>(src) + elem);
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
-      const float4 r = reinterpret_cast<const float4*>(src)[q];
+      const float4 r = v[q];
       x[4 * q] = r.x; x[4 * q + 1] = r.y; x[4 * q + 2] = r.z; x[4 * q + 3] = r.w;
     }
-    sum = __uint_as_float(src[32]);
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) x[i] = 0.0f;
+  }
+  __device__ __forceinline__ void prepare() {
+    float s = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) s += x[4 * q] + x[4 * q + 1] + x[4 * q + 2] + x[4 * q + 3];
+    sum = s;
   }
   __device__ __forceinline__ float apply(const uint4 w, float s, float b) const {
     return fmaf(s, q4_dot_f32(w, x), b * sum);
@@ -129,43 +112,29 @@ __device__ __forceinline__ void flag(uint32_t* status, uint32_t bits) {
   if (status != nullptr) atomicOr(status, bits);
 }
 
-// ------------------------------------------------------------- select -----
-// Softmax over the E logits of one token (fp32), gates rounded to the
-// activation type, top-K by (gate desc, index asc), renormalised scores.
-// One wave; lane k < K returns rank k.  Lanes hold experts lane + 64*m; each
-// lane sorts its keys, then K rounds take the wave-wide max of the list heads.
-
-template <class A>
-struct SelectKey {
-  using T = uint32_t;  // bf16: (gate bits << 16) | (0xffff - e); 0 = empty
-  __device__ static T make(float gate, uint32_t e) { return (f32_to_bf16(gate) << 16) | (0xffffu - e); }
-  __device__ static T wave_max(T v) { return wave_max_u32(v); }
-  __device__ static uint32_t expert(T k) { return 0xffffu - (k & 0xffffu); }
-  __device__ static float gate(T k) { return bf16_to_f32(k >> 16); }
-};
-
-template <>
-struct SelectKey<ActF32> {
-  using T = uint64_t;  // (gate bits << 32) | (0xffffffff - e)
-  __device__ static T make(float gate, uint32_t e) {
-    return (static_cast<uint64_t>(__float_as_uint(gate)) << 32) | (0xffffffffu - e);
-  }
-  __device__ static T wave_max(T v) {
-    const uint32_t hi = wave_max_u32(static_cast<uint32_t>(v >> 32));
-    const uint32_t lo = wave_max_u32(static_cast<uint32_t>(v >> 32) == hi ? static_cast<uint32_t>(v) : 0u);
-    return (static_cast<uint64_t>(hi) << 32) | lo;
-  }
-  __device__ static uint32_t expert(T k) { return 0xffffffffu - static_cast<uint32_t>(k); }
-  __device__ static float gate(T k) { return __uint_as_float(static_cast<uint32_t>(k >> 32)); }
-};
-
-template <class T>
-__device__ __forceinline__ void cas_desc(T& a, T& b) {
-  const T hi = a > b ? a : b;
-  const T lo = a > b ? b : a;
-  a = hi;
-  b = lo;
+__device__ __forceinline__ uint32_t mbcnt(uint64_t mask) {
+  return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                   __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0u));
 }
+
+// 1 KiB of zeros.  Lanes without data (tile tails, groups beyond the width,
+// unresolved routes, empty slots) load from here instead of skipping the
+// load: with the same number of loads on every path the compiler can wait for
+// one early load without waiting for all later ones, and no load waits inside
+// a branch.
+__device__ uint4 g_zero_page[64];
+
+// ------------------------------------------------------------- select -----
+// Router softmax in fp32 over the E logits of one token, gates rounded to the
+// activation type, then the top-K by (gate desc, index asc) and the
+// renormalised scores.  One wave; lane l holds experts l + 64 m (m < 8).
+//
+// Selection without a sort: gates are >= 0, so their bit patterns order like
+// their values.  A ballot binary search over the 64 lane maxima bounds the
+// K-th largest gate from below; the few gates at or above the bound are
+// compacted into LDS and ranked by comparing keys.  A block that runs one
+// routed pair keeps only its own rank; the block that publishes the
+// selection keeps all K.
 
 // exp(x) for x <= 0 as 2^(x*log2 e) on v_exp_f32, with the rounding error of
 // the product carried as a first-order correction (about 2 ulp in fp32).
@@ -178,108 +147,192 @@ __device__ __forceinline__ float exp_neg(float x) {
   return __builtin_amdgcn_exp2f(th) * fmaf(tl, kLn2, 1.0f);
 }
 
-// Orderable integer image of a float (monotone for all non-NaN values).
-__device__ __forceinline__ int float_order(float f) {
-  const int b = __float_as_int(f);
-  return b >= 0 ? b : (b ^ 0x7fffffff);
-}
+// Gate keys of one token: the gate's bit pattern (bf16: its upper 16 bits),
+// 0 for lanes beyond E.  Lower expert indices win ties, so padding lanes
+// (indices >= E) are never taken while K <= E.
+template <class A>
+struct GateKeys {
+  static constexpr int kShift = is_bf16<A>() ? 16 : 0;
+  static constexpr uint32_t kTop = 0x3f800000u >> kShift;  // key of gate 1.0
+  uint32_t k[kMaxExpertsPerLane];
+  __device__ static float gate(uint32_t key) { return __uint_as_float(key << kShift); }
+};
 
-__device__ __forceinline__ float order_float(int k) {
-  return __int_as_float(k >= 0 ? k : (k ^ 0x7fffffff));
-}
-
-__device__ __forceinline__ int wave_max_i32(int v) {
-  v = max(v, static_cast<int>(dpp_u<kDppQuadXor1>(static_cast<uint32_t>(v))));
-  v = max(v, static_cast<int>(dpp_u<kDppQuadXor2>(static_cast<uint32_t>(v))));
-  v = max(v, static_cast<int>(dpp_u<kDppHalfMirror>(static_cast<uint32_t>(v))));
-  v = max(v, static_cast<int>(dpp_u<kDppMirror>(static_cast<uint32_t>(v))));
-  const int t15 = __builtin_amdgcn_update_dpp(v, v, kDppBcast15, 0xA, 0xF, false);
-  v = max(v, t15);
-  const int t31 = __builtin_amdgcn_update_dpp(v, v, kDppBcast31, 0xC, 0xF, false);
-  v = max(v, t31);
-  return __builtin_amdgcn_readlane(v, 63);
-}
-
-template <class A, bool STORE_GATES>
-__device__ void select_topk(const float* logits, uint32_t E, uint32_t K, float blend, uint32_t lane,
-                            void* gates_out, int& my_e, float& my_score) {
-  using Key = SelectKey<A>;
-  using T = typename Key::T;
-  float l[kMaxExpertsPerLane];
-  int lmax_key = float_order(-FLT_MAX);
+// Lane l reads logits l + 64 m (clamped to E - 1, so every load is
+// unconditional); entries beyond E become -FLT_MAX.
+__device__ __forceinline__ void load_logits(const float* logits, uint32_t E, uint32_t lane,
+                                            float l[kMaxExpertsPerLane]) {
 #pragma unroll
   for (int m = 0; m < kMaxExpertsPerLane; ++m) {
-    const uint32_t e = lane + 64 * m;
-    l[m] = e < E ? logits[e] : -FLT_MAX;
-    lmax_key = max(lmax_key, float_order(l[m]));
+    const uint32_t e = lane + 64u * m;
+    const float v = logits[min(e, E - 1)];
+    l[m] = e < E ? v : -FLT_MAX;
   }
-  const float lmax = order_float(wave_max_i32(lmax_key));
+}
+
+template <class A>
+__device__ void softmax_keys(const float l[kMaxExpertsPerLane], uint32_t E, uint32_t lane, GateKeys<A>& g) {
+  float lmax = l[0];
+#pragma unroll
+  for (int m = 1; m < kMaxExpertsPerLane; ++m) lmax = fmaxf(lmax, l[m]);
+  lmax = wave_max_f32(lmax);
   float ex[kMaxExpertsPerLane];
   float local = 0.0f;
 #pragma unroll
   for (int m = 0; m < kMaxExpertsPerLane; ++m) {
-    ex[m] = lane + 64 * m < E ? exp_neg(l[m] - lmax) : 0.0f;
+    ex[m] = lane + 64u * m < E ? exp_neg(l[m] - lmax) : 0.0f;
     local += ex[m];
   }
   const float inv_total = 1.0f / wave_sum_all(local);
-  T key[kMaxExpertsPerLane];
 #pragma unroll
   for (int m = 0; m < kMaxExpertsPerLane; ++m) {
-    const uint32_t e = lane + 64 * m;
-    const float gate = A::round(ex[m] * inv_total);
-    if constexpr (STORE_GATES) {
-      if (e < E) A::store(gates_out, e, gate);
-    }
-    key[m] = e < E ? Key::make(gate, e) : T(0);
+    const uint32_t e = lane + 64u * m;
+    g.k[m] = e < E ? __float_as_uint(A::round(ex[m] * inv_total)) >> GateKeys<A>::kShift : 0u;
   }
-  // optimal 19-comparator sorting network for 8 keys, descending
-  cas_desc(key[0], key[1]); cas_desc(key[2], key[3]); cas_desc(key[4], key[5]); cas_desc(key[6], key[7]);
-  cas_desc(key[0], key[2]); cas_desc(key[1], key[3]); cas_desc(key[4], key[6]); cas_desc(key[5], key[7]);
-  cas_desc(key[1], key[2]); cas_desc(key[5], key[6]); cas_desc(key[0], key[4]); cas_desc(key[3], key[7]);
-  cas_desc(key[1], key[5]); cas_desc(key[2], key[6]);
-  cas_desc(key[1], key[4]); cas_desc(key[3], key[6]);
-  cas_desc(key[2], key[4]); cas_desc(key[3], key[5]);
-  cas_desc(key[3], key[4]);
-  float mass = 0.0f;
-  my_e = 0;
-  float my_gate = 0.0f;
-  for (uint32_t k = 0; k < K; ++k) {
-    const T win = Key::wave_max(key[0]);
-    const float g = Key::gate(win);
-    mass += g;
-    if (lane == k) {
-      my_e = static_cast<int>(Key::expert(win));
-      my_gate = g;
-    }
-    if (key[0] == win) {  // keys are unique: exactly one lane pops its head
+}
+
+// Number of keys >= v (wave-uniform).
+template <class A>
+__device__ __forceinline__ uint32_t count_ge(const GateKeys<A>& g, uint32_t v) {
+  uint32_t c = 0;
 #pragma unroll
-      for (int m = 0; m < kMaxExpertsPerLane - 1; ++m) key[m] = key[m + 1];
-      key[kMaxExpertsPerLane - 1] = T(0);
+  for (int m = 0; m < kMaxExpertsPerLane; ++m) c += __popcll(__ballot(g.k[m] >= v));
+  return c;
+}
+
+// Key of rank r: the largest v with more than r keys >= v.  `above` returns
+// the number of keys > v (at most r).
+template <class A>
+__device__ uint32_t rank_key(const GateKeys<A>& g, uint32_t r, uint32_t& above) {
+  uint32_t lo = 0, hi = GateKeys<A>::kTop + 1, c_hi = 0;  // count(>= lo) > r >= count(>= hi)
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    const uint32_t c = count_ge(g, mid);
+    if (c > r) {
+      lo = mid;
+    } else {
+      hi = mid;
+      c_hi = c;
     }
   }
-  // scores / (mass + blend * (selected_mass - mass)), each step rounded
+  above = c_hi;
+  return lo;
+}
+
+// Candidates of the top K.  The K largest lane maxima are K distinct gates,
+// so the K-th largest gate is at least the K-th largest lane maximum: every
+// gate >= that bound is a candidate.  When more than kMaxCand gates reach the
+// bound (many ties), the candidates are exactly the top K instead: the gates
+// above the K-th largest key plus the lowest-index ties at it.  Candidates go
+// to `cand` as (key << 32 | ~expert), which orders like (gate desc, index
+// asc).  Returns their number (K..kMaxCand).
+constexpr uint32_t kMaxCand = 64;
+
+template <class A>
+__device__ __forceinline__ uint32_t compact_candidates(const GateKeys<A>& g, uint32_t bound, uint32_t need,
+                                                       uint32_t lane, uint64_t* cand) {
+  uint32_t eq_before = 0, c = 0;
+#pragma unroll
+  for (int m = 0; m < kMaxExpertsPerLane; ++m) {
+    const uint32_t k = g.k[m];
+    const uint64_t eq = __ballot(k == bound);
+    const bool take = k > bound || (k == bound && eq_before + mbcnt(eq) < need);
+    const uint64_t sel = __ballot(take);
+    const uint32_t pos = c + mbcnt(sel);
+    if (take && pos < kMaxCand)
+      cand[pos] = (static_cast<uint64_t>(k) << 32) | (0xffffffffu - (lane + 64u * m));
+    eq_before += __popcll(eq);
+    c += __popcll(sel);
+  }
+  return c;
+}
+
+template <class A>
+__device__ uint32_t gather_candidates(const GateKeys<A>& g, uint32_t K, uint32_t lane, uint64_t* cand) {
+  uint32_t lmax = g.k[0];
+#pragma unroll
+  for (int m = 1; m < kMaxExpertsPerLane; ++m) lmax = max(lmax, g.k[m]);
+  uint32_t lo = 0, hi = GateKeys<A>::kTop + 1;  // count(lmax >= lo) >= K > count(lmax >= hi)
+  while (hi - lo > 1) {
+    const uint32_t mid = (lo + hi) >> 1;
+    if (static_cast<uint32_t>(__popcll(__ballot(lmax >= mid))) >= K) lo = mid; else hi = mid;
+  }
+  uint32_t c = compact_candidates(g, lo, 0xffffffffu, lane, cand);
+  if (c > kMaxCand) {
+    uint32_t above;
+    const uint32_t vk = rank_key(g, K - 1, above);
+    c = compact_candidates(g, vk, K - above, lane, cand);
+  }
+  __builtin_amdgcn_wave_barrier();
+  return c;
+}
+
+// Rank of candidate `lane` among the c candidates (0 = largest gate); lanes
+// >= c get `mine` = 0.
+__device__ __forceinline__ uint32_t candidate_rank(const uint64_t* cand, uint32_t c, uint32_t lane, uint64_t& mine) {
+  mine = lane < c ? cand[lane] : 0u;
+  uint32_t r = 0;
+#pragma unroll 4
+  for (uint32_t i = 0; i < c; ++i) r += cand[i] > mine ? 1u : 0u;
+  return r;
+}
+
+// Expert of rank r < K (wave-uniform).
+template <class A>
+__device__ uint32_t select_rank(const GateKeys<A>& g, uint32_t K, uint32_t r, uint32_t lane, uint64_t* cand) {
+  const uint32_t c = gather_candidates(g, K, lane, cand);
+  uint64_t mine;
+  const uint32_t rank = candidate_rank(cand, c, lane, mine);
+  const uint64_t hit = __ballot(lane < c && rank == r);
+  const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(hit));
+  return 0xffffffffu - static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine), src));
+}
+
+// The whole selection in rank order: lane k < K returns the expert of rank k
+// and its renormalised score.  scores = gate / (mass + blend*(selected_mass
+// - mass)), each step rounded to the activation type; the mass is summed in
+// rank order.
+template <class A>
+__device__ void rank_selection(const GateKeys<A>& g, uint32_t K, float blend, uint32_t lane, uint64_t* cand,
+                               uint32_t& e_out, float& score_out) {
+  const uint32_t c = gather_candidates(g, K, lane, cand);
+  uint64_t mine;
+  const uint32_t rank = candidate_rank(cand, c, lane, mine);
+  __builtin_amdgcn_wave_barrier();
+  if (lane < c && rank < K) cand[rank] = mine;
+  __builtin_amdgcn_wave_barrier();
+  float mass = 0.0f;
+  for (uint32_t i = 0; i < K; ++i) mass += GateKeys<A>::gate(static_cast<uint32_t>(cand[i] >> 32));
   mass = A::round(mass);
   const float diff = A::round(mass - mass);
   const float normalizer = A::round(mass + A::round(blend * diff));
-  my_score = A::round(my_gate / normalizer);
+  const uint64_t top = lane < K ? cand[lane] : 0u;
+  e_out = lane < K ? 0xffffffffu - static_cast<uint32_t>(top) : 0u;
+  score_out = lane < K ? A::round(GateKeys<A>::gate(static_cast<uint32_t>(top >> 32)) / normalizer) : 0.0f;
 }
-
-__global__ __launch_bounds__(64) void k_select_bf16(SelectLaunch p);
-__global__ __launch_bounds__(64) void k_select_f32(SelectLaunch p);
 
 template <class A>
 __device__ void select_body(const SelectLaunch& p) {
+  __shared__ uint64_t s_cand[kMaxCand];
   const uint32_t t = blockIdx.x;
   const uint32_t lane = threadIdx.x;
-  int e;
+  GateKeys<A> g;
+  float lg[kMaxExpertsPerLane];
+  load_logits(p.logits + static_cast<size_t>(t) * p.experts, p.experts, lane, lg);
+  softmax_keys<A>(lg, p.experts, lane, g);
+  if (p.gates != nullptr) {
+    void* gates = static_cast<char*>(p.gates) + static_cast<size_t>(t) * p.experts * A::kBytes;
+#pragma unroll
+    for (int m = 0; m < kMaxExpertsPerLane; ++m) {
+      const uint32_t e = lane + 64 * m;
+      if (e < p.experts) A::store(gates, e, GateKeys<A>::gate(g.k[m]));
+    }
+  }
+  uint32_t e;
   float score;
-  void* gates = p.gates == nullptr ? nullptr
-                                   : static_cast<char*>(p.gates) + static_cast<size_t>(t) * p.experts * A::kBytes;
-  const float* logits = p.logits + static_cast<size_t>(t) * p.experts;
-  if (gates != nullptr) select_topk<A, true>(logits, p.experts, p.top_k, p.blend, lane, gates, e, score);
-  else select_topk<A, false>(logits, p.experts, p.top_k, p.blend, lane, nullptr, e, score);
+  rank_selection<A>(g, p.top_k, p.blend, lane, s_cand, e, score);
   if (lane < p.top_k) {
-    p.inds[static_cast<size_t>(t) * p.top_k + lane] = e;
+    p.inds[static_cast<size_t>(t) * p.top_k + lane] = static_cast<int32_t>(e);
     A::store(p.scores, static_cast<size_t>(t) * p.top_k + lane, score);
   }
 }
@@ -364,15 +417,13 @@ __device__ void router_row(const FrontLaunch& p, uint32_t row, uint32_t lane) {
 template <class A>
 __device__ void shared_gate_logit(const FrontLaunch& p, uint32_t lane) {
   const uint32_t H = p.hidden, G = H / kGroup;
-  constexpr int GW = lds_group_words<A>();
   for (uint32_t t = 0; t < p.tokens; ++t) {
     float acc = 0.0f;
     for (uint32_t g = lane; g < G; g += 64) {
       const uint4 w = *reinterpret_cast<const uint4*>(p.seg.w + g * kWordsPerGroup);
-      uint32_t buf[GW];
-      stage_group<A>(p.x, static_cast<size_t>(t) * H + g * kGroup, buf);
       GroupAct<A> xa;
-      xa.load_lds(buf);
+      xa.fetch(p.x, static_cast<size_t>(t) * H + g * kGroup);
+      xa.prepare();
       acc += xa.apply(w, bf16_to_f32(p.seg.s[g]), bf16_to_f32(p.seg.b[g]));
     }
     const float logit = A::round(wave_sum_all(acc));
@@ -401,19 +452,50 @@ __global__ __launch_bounds__(kBlock) void k_front(FrontLaunch p, uint32_t router
 
 // ------------------------------------------------------------- gate/up ----
 
+__device__ __forceinline__ uint32_t route_word(int32_t slot) {
+  return slot >= 0 ? (kSlotBit | static_cast<uint32_t>(slot)) : kMissWord;
+}
+
+__device__ __forceinline__ void pin_proj(const ProjPtrs& q) {
+  VM_PIN(q.w);
+  VM_PIN(q.s);
+  VM_PIN(q.b);
+}
+
+template <int FIRST, int PARTS>
+__device__ __forceinline__ void pin_view(const PoolDev& v) {
+  VM_PIN(v.base);
+  VM_PIN(v.header);
+  VM_PIN(v.stride);
+  VM_PIN(v.records);
+#pragma unroll
+  for (int i = 0; i < PARTS; ++i) VM_PIN(v.off[FIRST + i]);
+}
+
+// SwiGLU of one row and the optional raw gate/up outputs.
+template <class A>
+__device__ __forceinline__ void gateup_store(const GateUpLaunch& p, uint32_t t, uint32_t j, uint32_t S, bool routed,
+                                             bool ok, uint32_t row, float g, float u) {
+  if (row >= p.inter) return;
+  const float gv = A::round(g);
+  const float uv = A::round(u);
+  A::store(p.act, (static_cast<size_t>(t) * S + j) * p.inter + row, ok ? swiglu_act<A>(gv, uv) : 0.0f);
+  if (routed) {
+    const size_t o = (static_cast<size_t>(t) * p.slots + j) * p.inter + row;
+    if (p.gate_out != nullptr) A::store(p.gate_out, o, gv);
+    if (p.up_out != nullptr) A::store(p.up_out, o, uv);
+  }
+}
+
+// LPR lanes per row (one 32-input group per lane and iteration, GI
+// iterations), U rows per lane group; a block covers RPB = (64/LPR)*U*4 rows.
 template <class A, int LPR, int GI, int U>
 __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RPW = RPI * U;
   constexpr int RPB = RPW * kWaves;
-  constexpr int GW = lds_group_words<A>();
-  extern __shared__ uint4 lds_raw[];
-  uint32_t* lds_x = reinterpret_cast<uint32_t*>(lds_raw);  // G * GW words
-  __shared__ int s_sel[kMaxTopK];
-  __shared__ float s_score[kMaxTopK];
-  __shared__ int s_table[kMaxExpertsPerLane * 64];
-  __shared__ float s_g[RPB], s_u[RPB];
-  __shared__ uint32_t s_word, s_ok;
+  __shared__ uint32_t s_word;
+  __shared__ uint64_t s_cand[kMaxCand];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -426,77 +508,57 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
   const uint32_t t = shared_pair ? pair - routed_pairs : pair / p.slots;
   const uint32_t j = shared_pair ? p.slots : pair % p.slots;
   const uint32_t S = p.slots + p.has_shared;
-  const uint32_t H = p.hidden, I = p.inter, G = H / kGroup;
+  const uint32_t H = p.hidden, I = p.inter, G = H / kGroup, E = p.experts;
   const bool select = !shared_pair && p.logits != nullptr;
   PhaseTrace tr;
   if (p.trace != nullptr) tr.mark(0);
+  pin_view<0, 6>(p.pool);
+  VM_PIN(p.act);
 
-  // prologue: expert selection (wave 0), slot table (wave 1), activations (rest)
+  // 1. loads: the selection's logits and slot-table entries first, then this
+  //    lane's activation groups
+  float lg[kMaxExpertsPerLane];
+  int32_t tab[kMaxExpertsPerLane];
   if (select && wave == 0) {
-    int e;
-    float score;
-    if (p.trace != nullptr) {  // when the logits arrive
-      const float first = p.logits[static_cast<size_t>(t) * p.experts + lane];
-      if (first == 12345.0f) s_score[0] = first;
-      tr.mark(5);
-    }
-    select_topk<A, false>(p.logits + static_cast<size_t>(t) * p.experts, p.experts, p.slots, p.blend, lane, nullptr, e,
-                   score);
-    if (p.trace != nullptr) {
-      tr.mark(6);
-      int e2;
-      float score2;
-      select_topk<A, false>(p.logits + static_cast<size_t>(t) * p.experts, p.experts, p.slots, p.blend, lane,
-                            nullptr, e2, score2);
-      if (e2 != e || score2 != score) s_score[0] = -1.0f;
-      tr.mark(9);
-    }
-    if (lane < p.slots) {
-      s_sel[lane] = e;
-      s_score[lane] = score;
+    load_logits(p.logits + static_cast<size_t>(t) * E, E, lane, lg);
+    if (p.slot_table != nullptr) {
+#pragma unroll
+      for (int m = 0; m < kMaxExpertsPerLane; ++m) tab[m] = p.slot_table[min(lane + 64u * m, E - 1)];
     }
   }
-  if (select && wave == 1 && p.slot_table != nullptr) {
-    for (uint32_t e = lane; e < p.experts; e += 64) s_table[e] = p.slot_table[e];
+  asm volatile("" ::: "memory");
+  GroupAct<A> xa[GI];
+#pragma unroll
+  for (int it = 0; it < GI; ++it) {
+    const uint32_t g = lr + it * LPR;
+    const bool live = g < G;
+    xa[it].fetch(live ? p.x : g_zero_page, live ? static_cast<size_t>(t) * H + g * kGroup : 0);
   }
-  const uint32_t first = select ? 2 * 64 : 0;
-  for (uint32_t g = tid - first; tid >= first && g < G; g += kBlock - first)
-    stage_group<A>(p.x, static_cast<size_t>(t) * H + g * kGroup, lds_x + g * GW);
-  if (tid == 0 && !select) {
-    if (shared_pair) {
-      s_ok = 1;
-    } else {
-      s_word = p.routes[t * p.slots + j];
-      s_ok = 1;
-    }
-  }
-  if (p.trace != nullptr) tr.mark(7);
-  __syncthreads();
-  if (p.trace != nullptr) tr.mark(8);
+
+  // 2. the route word of this pair
+  GateKeys<A> keys;
+  uint32_t word = 0;
   if (select) {
-    if (tid == 0) {
-      const int e = s_sel[j];
-      uint32_t word = static_cast<uint32_t>(e);
+    if (wave == 0) {
+      softmax_keys<A>(lg, E, lane, keys);
+      if (p.trace != nullptr) tr.mark(5);
+      const uint32_t e = select_rank<A>(keys, p.slots, j, lane, s_cand);
+      uint32_t w = e;
       if (p.slot_table != nullptr) {
-        const int slot = s_table[e];
-        word = slot >= 0 ? (kSlotBit | static_cast<uint32_t>(slot)) : kMissWord;
+        const uint32_t m_e = e >> 6, l_e = e & 63u;
+        int32_t slot = -1;
+#pragma unroll
+        for (int m = 0; m < kMaxExpertsPerLane; ++m)
+          if (m == static_cast<int>(m_e)) slot = __builtin_amdgcn_readlane(tab[m], l_e);
+        w = route_word(slot);
       }
-      s_word = word;
-    }
-    // one block per token publishes the selection for the down kernel
-    if (blockIdx.x == 0 && j == 0 && tid < p.slots) {
-      const size_t o = static_cast<size_t>(t) * p.slots + tid;
-      const int e = s_sel[tid];
-      uint32_t word = static_cast<uint32_t>(e);
-      if (p.slot_table != nullptr) {
-        const int slot = s_table[e];
-        word = slot >= 0 ? (kSlotBit | static_cast<uint32_t>(slot)) : kMissWord;
-      }
-      if (p.inds_out != nullptr) p.inds_out[o] = e;
-      if (p.scores_out != nullptr) A::store(p.scores_out, o, s_score[tid]);
-      if (p.words_out != nullptr) p.words_out[o] = word;
+      if (lane == 0) s_word = w;
+      if (p.trace != nullptr) tr.mark(6);
     }
     __syncthreads();
+    word = s_word;
+  } else if (!shared_pair) {
+    word = p.routes[t * p.slots + j];
   }
 
   ProjPtrs gp{}, upp{};
@@ -505,15 +567,20 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
     gp = p.shared_gate;
     upp = p.shared_up;
   } else {
-    const uint32_t word = s_word;
-    const int32_t* table = select ? nullptr : p.slot_table;
-    ok = resolve_proj(word, table, p.experts, p.pool, p.gate, 0, I, H, gp, &p.stream) &&
-         resolve_proj(word, table, p.experts, p.pool, p.up, 1, I, H, upp, &p.stream);
+    uint32_t index = 0;
+    const int kind = resolve_word(word, select ? nullptr : p.slot_table, E, p.pool, &p.stream,
+                                  p.gate.w != nullptr && p.up.w != nullptr, index);
+    ok = kind != kSrcNone;
+    source_proj(kind, index, p.pool, &p.stream, p.gate, 0, I, H, gp);
+    source_proj(kind, index, p.pool, &p.stream, p.up, 1, I, H, upp);
   }
   if (!ok && tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
   if (p.trace != nullptr) tr.mark(1);
 
+  // 3. stream the gate and up rows
   const uint32_t row_base = blockIdx.x * RPB + wave * RPW + rw;
+  const uint32_t* zw = reinterpret_cast<const uint32_t*>(g_zero_page) + lr * kWordsPerGroup;
+  const uint16_t* zm = reinterpret_cast<const uint16_t*>(g_zero_page) + lr;
   uint4 wg[U][GI], wu[U][GI];
   uint32_t sg[U][GI], bg[U][GI], su[U][GI], bu[U][GI];
   const size_t row_words = H / 8;
@@ -523,61 +590,65 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
 #pragma unroll
     for (int it = 0; it < GI; ++it) {
       const uint32_t g = lr + it * LPR;
-      if (ok && row < I && g < G) {
-        const size_t wo = row * row_words + g * kWordsPerGroup;
-        const size_t mo = static_cast<size_t>(row) * G + g;
-        wg[u][it] = *reinterpret_cast<const uint4*>(gp.w + wo);
-        wu[u][it] = *reinterpret_cast<const uint4*>(upp.w + wo);
-        sg[u][it] = gp.s[mo];
-        bg[u][it] = gp.b[mo];
-        su[u][it] = upp.s[mo];
-        bu[u][it] = upp.b[mo];
-      } else {
-        wg[u][it] = wu[u][it] = make_uint4(0, 0, 0, 0);
-        sg[u][it] = bg[u][it] = su[u][it] = bu[u][it] = 0;
-      }
+      const bool live = ok && row < I && g < G;
+      const size_t wo = static_cast<size_t>(row) * row_words + g * kWordsPerGroup;
+      const size_t mo = static_cast<size_t>(row) * G + g;
+      wg[u][it] = ldg16(live ? gp.w + wo : zw);
+      wu[u][it] = ldg16(live ? upp.w + wo : zw);
+      sg[u][it] = ldg_u16(live ? gp.s + mo : zm);
+      bg[u][it] = ldg_u16(live ? gp.b + mo : zm);
+      su[u][it] = ldg_u16(live ? upp.s + mo : zm);
+      bu[u][it] = ldg_u16(live ? upp.b + mo : zm);
     }
   }
-  GroupAct<A> xa[GI];
-#pragma unroll
-  for (int it = 0; it < GI; ++it) {
-    const uint32_t g = lr + it * LPR;
-    xa[it].load_lds(lds_x + (g < G ? g : 0) * GW);
+
+  // 4. one block per token publishes the ordered selection for the down kernel
+  if (select && blockIdx.x == 0 && j == 0 && wave == 0) {
+    uint32_t e;
+    float score;
+    rank_selection<A>(keys, p.slots, p.blend, lane, s_cand, e, score);
+    if (lane < p.slots) {
+      const size_t o = static_cast<size_t>(t) * p.slots + lane;
+      if (p.inds_out != nullptr) p.inds_out[o] = static_cast<int32_t>(e);
+      if (p.scores_out != nullptr) A::store(p.scores_out, o, score);
+      if (p.words_out != nullptr) p.words_out[o] = p.slot_table != nullptr ? route_word(p.slot_table[e]) : e;
+    }
   }
+
+  // 5. group dots, row sums, SwiGLU
+#pragma unroll
+  for (int it = 0; it < GI; ++it) xa[it].prepare();
+  float gs[U], us[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     float ag = 0.0f, au = 0.0f;
 #pragma unroll
     for (int it = 0; it < GI; ++it) {
-      if (lr + it * LPR < G) {
-        ag += xa[it].apply(wg[u][it], bf16_to_f32(sg[u][it]), bf16_to_f32(bg[u][it]));
-        au += xa[it].apply(wu[u][it], bf16_to_f32(su[u][it]), bf16_to_f32(bu[u][it]));
-      }
+      ag += xa[it].apply(wg[u][it], bf16_to_f32(sg[u][it]), bf16_to_f32(bg[u][it]));
+      au += xa[it].apply(wu[u][it], bf16_to_f32(su[u][it]), bf16_to_f32(bu[u][it]));
     }
-    ag = group_sum<LPR>(ag);
-    au = group_sum<LPR>(au);
-    if (lr == LPR - 1) {
-      const uint32_t r = wave * RPW + rw + u * RPI;
-      s_g[r] = ag;
-      s_u[r] = au;
-    }
+    gs[u] = group_sum<LPR>(ag);
+    us[u] = group_sum<LPR>(au);
     if (u == 0 && p.trace != nullptr) tr.mark(2);
   }
   if (p.trace != nullptr) tr.mark(3);
-  __syncthreads();
-  // block-parallel epilogue: one thread per row
-  if (tid < RPB) {
-    const uint32_t row = blockIdx.x * RPB + (tid / RPW) * RPW + tid % RPW;
-    if (row < I) {
-      const float gv = A::round(s_g[tid]);
-      const float uv = A::round(s_u[tid]);
-      const size_t act_base = (static_cast<size_t>(t) * S + j) * I;
-      A::store(p.act, act_base + row, ok ? swiglu_act<A>(gv, uv) : 0.0f);
-      if (!shared_pair) {
-        const size_t o = (static_cast<size_t>(t) * p.slots + j) * I + row;
-        if (p.gate_out != nullptr) A::store(p.gate_out, o, gv);
-        if (p.up_out != nullptr) A::store(p.up_out, o, uv);
+  if constexpr (LPR == 64) {
+    // the U row sums sit in lane 63: lane u takes row u
+    float gv = 0.0f, uv = 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float a = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, gs[u]), 63));
+      const float b = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, us[u]), 63));
+      if (lane == static_cast<uint32_t>(u)) {
+        gv = a;
+        uv = b;
       }
+    }
+    if (lane < static_cast<uint32_t>(U)) gateup_store<A>(p, t, j, S, !shared_pair, ok, row_base + lane, gv, uv);
+  } else {
+    if (lr == LPR - 1) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) gateup_store<A>(p, t, j, S, !shared_pair, ok, row_base + u * RPI, gs[u], us[u]);
     }
   }
   if (p.trace != nullptr && tid == 0) {
@@ -588,17 +659,16 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
 
 // ----------------------------------------------------------------- down ---
 
-constexpr int kDownMaxSlots = 12;  // MAX_TOP_K (10) + shared, rounded up
-constexpr int kDownQuads = 2;      // row groups of 64/LPR rows per block
-constexpr int kDownMaxUnits = (kDownMaxSlots * kDownQuads + kWaves - 1) / kWaves;
+constexpr int kDownMaxSlots = 12;                         // MAX_TOP_K (10) + shared, rounded up
+constexpr int kDownSlotsPerWave = kDownMaxSlots / kWaves;  // wave w owns slots w, w+4, w+8
+constexpr int kDownQuads = 2;                             // row groups of 64/LPR rows per block
 
+// LPR = I/32 lanes per row (one group each); a block covers RB rows of all
+// slots of one token.
 template <class A, int LPR>
 __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RB = RPI * kDownQuads;
-  constexpr int GW = lds_group_words<A>();
-  extern __shared__ uint4 lds_raw[];
-  uint32_t* lds_act = reinterpret_cast<uint32_t*>(lds_raw);
   __shared__ float s_part[kDownMaxSlots * RB];
   __shared__ float s_scores[kDownMaxSlots];
   __shared__ float s_shared[RB];
@@ -616,60 +686,70 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   const uint32_t row0 = blockIdx.x * RB;
   PhaseTrace tr;
   if (p.trace != nullptr) tr.mark(0);
+  pin_view<6, 3>(p.pool);
+  pin_proj(p.shared_down);
+  VM_PIN(p.act);
 
-  // 1. lane k < K resolves slot k once (one load latency for all slots), the
-  //    units take their pointers with readlane and issue their weight loads
-  ProjPtrs mine{};
-  bool mine_ok = false;
-  if (lane < K) {
-    mine_ok = resolve_proj(p.routes[t * K + lane], p.slot_table, p.experts, p.pool, p.down, 2, H, I, mine,
-                           &p.stream);
-    if (!mine_ok && wave == 0 && blockIdx.x == 0) flag(p.status, 1u);
+  // 1. loads: the route words first (lane k < K reads slot k), then this
+  //    wave's activation groups (slot wave + 4 i, group lr)
+  const uint32_t route = ldg_u32(p.routes + static_cast<size_t>(t) * K + min(lane, K - 1));
+  asm volatile("" ::: "memory");
+  GroupAct<A> xa[kDownSlotsPerWave];
+#pragma unroll
+  for (int i = 0; i < kDownSlotsPerWave; ++i) {
+    const uint32_t slot = wave + kWaves * i;
+    const bool live = slot < S && lr < G;
+    xa[i].fetch(live ? p.act : g_zero_page, live ? (static_cast<size_t>(t) * S + slot) * I + lr * kGroup : 0);
   }
+
+  // 2. lane k < K resolves slot k; the waves take their slots' pointers with
+  //    readlane and issue their weight loads
+  ProjPtrs mine{};
+  uint32_t index = 0;
+  const int kind = lane < K ? resolve_word(route, p.slot_table, p.experts, p.pool, &p.stream, p.down.w != nullptr,
+                                           index)
+                            : kSrcNone;
+  source_proj(kind, index, p.pool, &p.stream, p.down, 2, H, I, mine);
+  const bool mine_ok = kind != kSrcNone;
+  if (!mine_ok && lane < K && wave == 0 && blockIdx.x == 0) flag(p.status, 1u);
   const uint64_t ok_mask = __ballot(mine_ok);
   if (p.trace != nullptr) tr.mark(5);
-  uint4 w[kDownMaxUnits];
-  uint32_t sc[kDownMaxUnits], bi[kDownMaxUnits];
+  const uint32_t* zw = reinterpret_cast<const uint32_t*>(g_zero_page) + lr * kWordsPerGroup;
+  const uint16_t* zm = reinterpret_cast<const uint16_t*>(g_zero_page) + lr;
+  uint4 w[kDownSlotsPerWave][kDownQuads];
+  uint32_t sc[kDownSlotsPerWave][kDownQuads], bi[kDownSlotsPerWave][kDownQuads];
   const size_t row_words = I / 8;
 #pragma unroll
-  for (int i = 0; i < kDownMaxUnits; ++i) {
-    const uint32_t unit = wave + kWaves * i;
-    const uint32_t slot = unit / kDownQuads;
-    const uint32_t quad = unit % kDownQuads;
-    const uint32_t row = row0 + quad * RPI + rw;
+  for (int i = 0; i < kDownSlotsPerWave; ++i) {
+    const uint32_t slot = wave + kWaves * i;
+    if (slot >= S) break;  // wave-uniform
     ProjPtrs dp{};
-    bool ok = false;
-    if (unit < S * kDownQuads) {
-      if (slot < K) {
-        ok = (ok_mask >> slot) & 1u;
-        dp.w = reinterpret_cast<const uint32_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.w), slot));
-        dp.s = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.s), slot));
-        dp.b = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.b), slot));
-      } else {
-        dp = p.shared_down;
-        ok = true;
-      }
-    }
-    if (ok && row < H && lr < G) {
-      w[i] = *reinterpret_cast<const uint4*>(dp.w + row * row_words + lr * kWordsPerGroup);
-      sc[i] = dp.s[static_cast<size_t>(row) * G + lr];
-      bi[i] = dp.b[static_cast<size_t>(row) * G + lr];
+    bool ok;
+    if (slot < K) {
+      ok = (ok_mask >> slot) & 1u;
+      dp.w = reinterpret_cast<const uint32_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.w), slot));
+      dp.s = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.s), slot));
+      dp.b = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.b), slot));
     } else {
-      w[i] = make_uint4(0, 0, 0, 0);
-      sc[i] = bi[i] = 0;
+      dp = p.shared_down;
+      ok = true;
+    }
+#pragma unroll
+    for (int q = 0; q < kDownQuads; ++q) {
+      const uint32_t row = row0 + q * RPI + rw;
+      const bool live = ok && row < H && lr < G;
+      const size_t mo = static_cast<size_t>(row) * G + lr;
+      w[i][q] = ldg16(live ? dp.w + static_cast<size_t>(row) * row_words + lr * kWordsPerGroup : zw);
+      sc[i][q] = ldg_u16(live ? dp.s + mo : zm);
+      bi[i][q] = ldg_u16(live ? dp.b + mo : zm);
     }
   }
   if (p.trace != nullptr) tr.mark(6);
 
-  // 2. stage the token's activations (all slots) into LDS; prefetch the epilogue operands
-  for (uint32_t item = tid; item < S * G; item += kBlock) {
-    const uint32_t slot = item / G, g = item % G;
-    stage_group<A>(p.act, (static_cast<size_t>(t) * S + slot) * I + g * kGroup, lds_act + item * GW);
-  }
-  if (p.trace != nullptr) tr.mark(7);
+  // 3. epilogue operands
   if (p.scores != nullptr) {
     if (tid < K) s_scores[tid] = load_any(p.scores, static_cast<size_t>(t) * K + tid, p.score_dtype);
-    const uint32_t r = tid - 64;  // wave 1 prefetches the shared term of the tile
+    const uint32_t r = tid - 64;  // wave 1 fetches the shared term of the tile
     if (tid >= 64 && r < RB && row0 + r < H) {
       const size_t o = static_cast<size_t>(t) * H + row0 + r;
       if (p.shared_y != nullptr) s_shared[r] = A::load(p.shared_y, o);
@@ -680,31 +760,27 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
       else if (p.shared != nullptr) s_sig = A::load(p.shared_gate, t);
     }
   }
-  if (p.trace != nullptr) tr.mark(8);
-  __syncthreads();
-  if (p.trace != nullptr) tr.mark(1);
+  if (p.trace != nullptr) tr.mark(7);
 
-  // 3. dot products, row sums, partials to LDS
+  // 4. dot products and row sums into LDS
 #pragma unroll
-  for (int i = 0; i < kDownMaxUnits; ++i) {
-    const uint32_t unit = wave + kWaves * i;
-    if (unit >= S * kDownQuads) break;  // wave-uniform
-    const uint32_t slot = unit / kDownQuads;
-    const uint32_t quad = unit % kDownQuads;
-    float v = 0.0f;
-    if (lr < G) {
-      GroupAct<A> xa;
-      xa.load_lds(lds_act + (slot * G + lr) * GW);
-      v = xa.apply(w[i], bf16_to_f32(sc[i]), bf16_to_f32(bi[i]));
+  for (int i = 0; i < kDownSlotsPerWave; ++i) {
+    const uint32_t slot = wave + kWaves * i;
+    if (slot >= S) break;  // wave-uniform
+    xa[i].prepare();
+#pragma unroll
+    for (int q = 0; q < kDownQuads; ++q) {
+      float v = xa[i].apply(w[i][q], bf16_to_f32(sc[i][q]), bf16_to_f32(bi[i][q]));
+      v = group_sum<LPR>(v);
+      if (lr == LPR - 1) s_part[slot * RB + q * RPI + rw] = v;
     }
-    v = group_sum<LPR>(v);
-    if (lr == LPR - 1) s_part[slot * RB + quad * RPI + rw] = v;
     if (i == 0 && p.trace != nullptr) tr.mark(2);
   }
   if (p.trace != nullptr) tr.mark(3);
   __syncthreads();
+  if (p.trace != nullptr) tr.mark(1);
 
-  // 4. epilogue
+  // 5. combine in slot order
   if (p.scores != nullptr) {
     if (tid < RB && row0 + tid < H) {
       const uint32_t r = tid;
@@ -759,30 +835,27 @@ uint32_t next_pow2(uint32_t v) {
   return r;
 }
 
-template <class K>
-hipError_t ensure_lds(K* kernel, size_t bytes, size_t& granted) {
-  if (bytes > granted) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
-    if (e != hipSuccess) return e;
-    granted = bytes;
-  }
-  return hipSuccess;
+// One kernel launch of a timing family; with timing on, the start/stop events
+// ride on the dispatch itself.
+template <class... KArgs, class... Args>
+hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
+                  Args... args) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (timing_events(family, &start, &stop))
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+  return hipGetLastError();
 }
 
 template <class A, int LPR, int GI, int U>
 hipError_t gateup_go(const GateUpLaunch& p, hipStream_t stream) {
   constexpr int RPB = (64 / LPR) * U * kWaves;
   const uint32_t pairs = p.tokens * p.slots + (p.has_shared ? p.tokens : 0);
-  const size_t lds = static_cast<size_t>(p.hidden / kGroup) * lds_group_words<A>() * 4;
-  static size_t granted = 48 * 1024;
-  hipError_t e = ensure_lds(&k_gateup<A, LPR, GI, U>, lds, granted);
-  if (e != hipSuccess) return e;
   dim3 grid((p.inter + RPB - 1) / RPB, pairs);
   GateUpLaunch q = p;
   q.trace = trace_reserve(grid.x * grid.y);
-  hipLaunchKernelGGL((k_gateup<A, LPR, GI, U>), grid, dim3(kBlock), lds, stream, q);
-  return hipGetLastError();
+  return launch("gateup", k_gateup<A, LPR, GI, U>, grid, dim3(kBlock), stream, q);
 }
 
 template <class A>
@@ -799,28 +872,18 @@ hipError_t gateup_dispatch(const GateUpLaunch& p, hipStream_t stream) {
     case 32: return gateup_go<A, 32, 1, 2>(p, stream);
     default: break;
   }
-  if (gi <= 1) return gateup_go<A, 64, 1, 2>(p, stream);
+  if (gi <= 1) return gateup_go<A, 64, 1, 4>(p, stream);
   if (gi <= 2) return gateup_go<A, 64, 2, 2>(p, stream);
   return gateup_go<A, 64, 4, 1>(p, stream);
-}
-
-template <class A>
-size_t down_lds_bytes(uint32_t slots_total, uint32_t inter) {
-  return static_cast<size_t>(slots_total) * (inter / kGroup) * lds_group_words<A>() * 4;
 }
 
 template <class A, int LPR>
 hipError_t down_go(const DownLaunch& p, hipStream_t stream) {
   constexpr int RB = (64 / LPR) * kDownQuads;
-  const size_t lds = down_lds_bytes<A>(p.slots + p.has_shared, p.inter);
-  static size_t granted = 48 * 1024;
-  hipError_t e = ensure_lds(&k_down<A, LPR>, lds, granted);
-  if (e != hipSuccess) return e;
   dim3 grid((p.hidden + RB - 1) / RB, p.tokens);
   DownLaunch q = p;
   q.trace = trace_reserve(grid.x * grid.y);
-  hipLaunchKernelGGL((k_down<A, LPR>), grid, dim3(kBlock), lds, stream, q);
-  return hipGetLastError();
+  return launch("down", k_down<A, LPR>, grid, dim3(kBlock), stream, q);
 }
 
 template <class A>
@@ -837,17 +900,18 @@ hipError_t down_dispatch(const DownLaunch& p, hipStream_t stream) {
 }
 
 template <class A>
-void front_go(const FrontLaunch& p0, hipStream_t stream) {
+hipError_t front_go(const FrontLaunch& p0, hipStream_t stream) {
   const uint32_t router_blocks = (p0.experts + kWaves - 1) / kWaves;
   const uint32_t blocks = router_blocks + (p0.seg.w != nullptr ? 1 : 0);
   FrontLaunch p = p0;
   p.trace = trace_reserve(blocks);
   const uint32_t chunks = (p.hidden / 8 + 63) / 64;
-  if (chunks <= 1) hipLaunchKernelGGL((k_front<A, 1>), dim3(blocks), dim3(kBlock), 0, stream, p, router_blocks);
-  else if (chunks <= 2) hipLaunchKernelGGL((k_front<A, 2>), dim3(blocks), dim3(kBlock), 0, stream, p, router_blocks);
-  else if (chunks <= 4) hipLaunchKernelGGL((k_front<A, 4>), dim3(blocks), dim3(kBlock), 0, stream, p, router_blocks);
-  else if (chunks <= 8) hipLaunchKernelGGL((k_front<A, 8>), dim3(blocks), dim3(kBlock), 0, stream, p, router_blocks);
-  else hipLaunchKernelGGL((k_front<A, 16>), dim3(blocks), dim3(kBlock), 0, stream, p, router_blocks);
+  const dim3 grid(blocks), block(kBlock);
+  if (chunks <= 1) return launch("router", k_front<A, 1>, grid, block, stream, p, router_blocks);
+  if (chunks <= 2) return launch("router", k_front<A, 2>, grid, block, stream, p, router_blocks);
+  if (chunks <= 4) return launch("router", k_front<A, 4>, grid, block, stream, p, router_blocks);
+  if (chunks <= 8) return launch("router", k_front<A, 8>, grid, block, stream, p, router_blocks);
+  return launch("router", k_front<A, 16>, grid, block, stream, p, router_blocks);
 }
 
 }  // namespace
@@ -856,61 +920,39 @@ bool gateup_supported(uint32_t hidden) {
   return hidden % kGroup == 0 && hidden > 0 && hidden / kGroup <= 256;
 }
 
-bool down_supported(uint32_t inter, uint32_t slots_total, int act_dtype) {
+bool down_supported(uint32_t inter, uint32_t slots_total, int /*act_dtype*/) {
   if (inter % kGroup != 0 || inter == 0 || inter / kGroup > 64) return false;
-  if (slots_total > static_cast<uint32_t>(kDownMaxSlots) || slots_total == 0) return false;
-  const size_t lds = act_dtype == 0 ? down_lds_bytes<ActBF16>(slots_total, inter)
-                                    : down_lds_bytes<ActF32>(slots_total, inter);
-  return lds <= 128 * 1024;
+  return slots_total > 0 && slots_total <= static_cast<uint32_t>(kDownMaxSlots);
 }
 
 hipError_t launch_front(const FrontLaunch& p, hipStream_t stream) {
-  timing_begin("router", stream);
-  if (p.act_dtype == 0) front_go<ActBF16>(p, stream); else front_go<ActF32>(p, stream);
-  hipError_t e = hipGetLastError();
-  timing_end("router", stream);
-  return e;
+  return p.act_dtype == 0 ? front_go<ActBF16>(p, stream) : front_go<ActF32>(p, stream);
 }
 
 hipError_t launch_select(const SelectLaunch& p, hipStream_t stream) {
-  timing_begin("select", stream);
-  if (p.act_dtype == 0) hipLaunchKernelGGL(k_select_bf16, dim3(p.tokens), dim3(64), 0, stream, p);
-  else hipLaunchKernelGGL(k_select_f32, dim3(p.tokens), dim3(64), 0, stream, p);
-  hipError_t e = hipGetLastError();
-  timing_end("select", stream);
-  return e;
+  const dim3 grid(p.tokens), block(64);
+  return p.act_dtype == 0 ? launch("select", k_select_bf16, grid, block, stream, p)
+                          : launch("select", k_select_f32, grid, block, stream, p);
 }
 
 hipError_t launch_gateup(const GateUpLaunch& p, hipStream_t stream) {
-  timing_begin("gateup", stream);
-  hipError_t e = p.act_dtype == 0 ? gateup_dispatch<ActBF16>(p, stream) : gateup_dispatch<ActF32>(p, stream);
-  timing_end("gateup", stream);
-  return e;
+  return p.act_dtype == 0 ? gateup_dispatch<ActBF16>(p, stream) : gateup_dispatch<ActF32>(p, stream);
 }
 
 hipError_t launch_down(const DownLaunch& p, hipStream_t stream) {
-  timing_begin("down", stream);
-  hipError_t e = p.act_dtype == 0 ? down_dispatch<ActBF16>(p, stream) : down_dispatch<ActF32>(p, stream);
-  timing_end("down", stream);
-  return e;
+  return p.act_dtype == 0 ? down_dispatch<ActBF16>(p, stream) : down_dispatch<ActF32>(p, stream);
 }
 
 hipError_t launch_weighted_combine(const void* values, const void* scores, void* out, uint32_t tokens,
                                    uint32_t slots, uint32_t hidden, int act_dtype, int score_dtype,
                                    hipStream_t stream) {
   const size_t n = static_cast<size_t>(tokens) * hidden;
-  const uint32_t blocks = static_cast<uint32_t>((n + kBlock - 1) / kBlock);
-  timing_begin("combine", stream);
-  if (act_dtype == 0) {
-    hipLaunchKernelGGL(k_weighted_combine<ActBF16>, dim3(blocks), dim3(kBlock), 0, stream, values, scores, out,
-                       tokens, slots, hidden, score_dtype);
-  } else {
-    hipLaunchKernelGGL(k_weighted_combine<ActF32>, dim3(blocks), dim3(kBlock), 0, stream, values, scores, out,
-                       tokens, slots, hidden, score_dtype);
-  }
-  hipError_t e = hipGetLastError();
-  timing_end("combine", stream);
-  return e;
+  const dim3 grid(static_cast<uint32_t>((n + kBlock - 1) / kBlock)), block(kBlock);
+  if (act_dtype == 0)
+    return launch("combine", k_weighted_combine<ActBF16>, grid, block, stream, values, scores, out, tokens, slots,
+                  hidden, score_dtype);
+  return launch("combine", k_weighted_combine<ActF32>, grid, block, stream, values, scores, out, tokens, slots,
+                hidden, score_dtype);
 }
 
 }  // namespace vm

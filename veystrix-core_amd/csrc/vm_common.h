@@ -19,12 +19,10 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
-// Round-to-nearest-even float -> bf16 bits; NaN stays a quiet NaN.
+// Round-to-nearest-even float -> bf16 bits (gfx950 v_cvt_pk_bf16_f32); NaN
+// stays a quiet NaN.
 __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -58,6 +56,31 @@ struct ActF32 {
 __device__ __forceinline__ float load_any(const void* p, size_t i, uint32_t dtype) {
   return dtype == 0 ? ActBF16::load(p, i) : ActF32::load(p, i);
 }
+
+// ------------------------------------------------------- global loads ---
+// Loads through an explicit global-address-space pointer.  A pointer that
+// went through readlane or a select is generic to the compiler, and generic
+// (flat) loads also count on the LDS/scalar counter, so every LDS access or
+// kernel-argument read after them waits for the whole stream.
+typedef unsigned int vm_u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint4 ldg16(const void* p) {
+  const vm_u32x4 v = *(const __attribute__((address_space(1))) vm_u32x4*)(p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t ldg_u16(const void* p) {
+  return *(const __attribute__((address_space(1))) unsigned short*)(p);
+}
+
+__device__ __forceinline__ uint32_t ldg_u32(const void* p) {
+  return *(const __attribute__((address_space(1))) unsigned int*)(p);
+}
+
+// Materialises a kernel-argument value in SGPRs at this point.  Members of a
+// by-value kernel argument are otherwise read at their first use, which puts
+// one scalar-load round trip per use on the critical path.
+#define VM_PIN(value) asm volatile("" ::"s"(value))
 
 // ---------------------------------------------------------- activations --
 // MLX's stable sigmoid sequence, every step rounded to the activation type
@@ -234,36 +257,60 @@ __device__ __forceinline__ void record_parts(const PoolDev& view, uint32_t recor
   out.b = reinterpret_cast<const uint16_t*>(rec + view.off[3 * proj + 2]);
 }
 
-// Resolve the projection `proj` (0 gate, 1 up, 2 down) of one route word.
-// Returns false (and leaves `out` untouched) when the word addresses nothing.
+// Where a route word points.  With a slot table the word is an expert id
+// mapped to a pool slot; otherwise a word with the slot bit is a pool slot,
+// and a plain word is a record of the stream view when one is given, else a
+// dense expert index.
+enum : int { kSrcNone = 0, kSrcPool = 1, kSrcStream = 2, kSrcDense = 3 };
+
+__device__ __forceinline__ int resolve_word(uint32_t word, const int32_t* slot_table, uint32_t experts,
+                                            const PoolDev& pool, const PoolDev* stream, bool has_dense,
+                                            uint32_t& index) {
+  if (slot_table != nullptr) {
+    if (word >= experts) return kSrcNone;
+    const int32_t slot = slot_table[word];
+    if (slot < 0 || static_cast<uint32_t>(slot) >= pool.records) return kSrcNone;
+    index = static_cast<uint32_t>(slot);
+    return kSrcPool;
+  }
+  if (word & kSlotBit) {
+    index = word & ~kSlotBit;
+    return pool.base != nullptr && index < pool.records ? kSrcPool : kSrcNone;
+  }
+  index = word;
+  if (stream != nullptr && stream->base != nullptr) return word < stream->records ? kSrcStream : kSrcNone;
+  return has_dense && word < experts ? kSrcDense : kSrcNone;
+}
+
+// Pointers of projection `proj` (0 gate, 1 up, 2 down; rows x in_width) of a
+// resolved source.
+__device__ __forceinline__ void source_proj(int kind, uint32_t index, const PoolDev& pool, const PoolDev* stream,
+                                            const ProjPtrs& dense, int proj, uint32_t rows, uint32_t in_width,
+                                            ProjPtrs& out) {
+  if (kind == kSrcPool) {
+    record_parts(pool, index, proj, out);
+  } else if (kind == kSrcStream) {
+    record_parts(*stream, index, proj, out);
+  } else if (kind == kSrcDense) {
+    const size_t words = static_cast<size_t>(rows) * (in_width / 8);
+    const size_t meta = static_cast<size_t>(rows) * (in_width / kGroup);
+    out.w = dense.w + static_cast<size_t>(index) * words;
+    out.s = dense.s + static_cast<size_t>(index) * meta;
+    out.b = dense.b + static_cast<size_t>(index) * meta;
+  }
+}
+
+// Resolve the projection `proj` of one route word.  Returns false (and
+// leaves `out` untouched) when the word addresses nothing.
 __device__ __forceinline__ bool resolve_proj(uint32_t word, const int32_t* slot_table,
                                              uint32_t experts, const PoolDev& pool,
                                              const ProjPtrs& dense, int proj, uint32_t rows,
                                              uint32_t in_width, ProjPtrs& out,
                                              const PoolDev* stream = nullptr) {
-  uint32_t record;
-  if (slot_table != nullptr) {
-    if (word >= experts) return false;
-    const int32_t slot = slot_table[word];
-    if (slot < 0 || static_cast<uint32_t>(slot) >= pool.records) return false;
-    record = static_cast<uint32_t>(slot);
-  } else if (word & kSlotBit) {
-    record = word & ~kSlotBit;
-    if (pool.base == nullptr || record >= pool.records) return false;
-  } else if (stream != nullptr && stream->base != nullptr) {
-    if (word >= stream->records) return false;
-    record_parts(*stream, word, proj, out);
-    return true;
-  } else {
-    if (word >= experts || dense.w == nullptr) return false;
-    const size_t words = static_cast<size_t>(rows) * (in_width / 8);
-    const size_t meta = static_cast<size_t>(rows) * (in_width / kGroup);
-    out.w = dense.w + static_cast<size_t>(word) * words;
-    out.s = dense.s + static_cast<size_t>(word) * meta;
-    out.b = dense.b + static_cast<size_t>(word) * meta;
-    return true;
-  }
-  record_parts(pool, record, proj, out);
+  uint32_t index = 0;
+  const int kind = resolve_word(word, slot_table, experts, pool, stream, dense.w != nullptr, index);
+  if (kind == kSrcNone) return false;
+  source_proj(kind, index, pool, stream, dense, proj, rows, in_width, out);
   return true;
 }
 

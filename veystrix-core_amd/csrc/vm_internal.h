@@ -93,9 +93,10 @@ hipError_t launch_weighted_combine(const void* values, const void* scores, void*
 bool gateup_supported(uint32_t hidden);
 bool down_supported(uint32_t inter, uint32_t slots_total, int act_dtype);
 
-// Kernel timing hooks (api.hip).
-void timing_begin(const char* family, hipStream_t stream);
-void timing_end(const char* family, hipStream_t stream);
+// Kernel timing (api.hip): when timing is on, returns the start/stop events
+// to attach to the next launch of `family` (hipExtLaunchKernelGGL stamps them
+// when the kernel starts and ends) and queues them for vm_timing_read.
+bool timing_events(const char* family, hipEvent_t* start, hipEvent_t* stop);
 // Phase-trace records for a launch of `blocks` blocks (null when tracing is off or full).
 uint64_t* trace_reserve(uint32_t blocks);
 
