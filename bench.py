@@ -42,7 +42,7 @@ def log(msg):
 def build_stack(spec, layers, device, seed):
     import torch
 
-    from veymoe import assemble
+    from veymoe import assemble, synth
     from veymoe.layer import HipSwitchGLU, MoELayer, QuantizedMLP, RouterLinear
     from veymoe.executor import Q4G32Projection
     from veymoe.pool import ExpertPool
@@ -71,10 +71,12 @@ def build_stack(spec, layers, device, seed):
     stack = []
     for layer in range(layers):
         router = (torch.randn((spec.experts, spec.hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
+        bias = synth.router_bias(spec, seed, layer)   # log Zipf(s) popularity when the spec asks for it
+        bias = None if bias is None else torch.from_numpy(bias).to(device)
         shared = QuantizedMLP(q4(1, spec.shared_inter, spec.hidden), q4(1, spec.shared_inter, spec.hidden),
                               q4(1, spec.hidden, spec.shared_inter))
         switch = HipSwitchGLU(spec.hidden, spec.inter, spec.experts, pool=pool, layer_id=layer)
-        stack.append(MoELayer(RouterLinear(router), switch, spec.top_k, shared_expert=shared,
+        stack.append(MoELayer(RouterLinear(router, bias), switch, spec.top_k, shared_expert=shared,
                               shared_expert_gate=q4(1, 1, spec.hidden)))
     return stack, pool
 

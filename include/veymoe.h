@@ -155,11 +155,17 @@ typedef struct VmRouterArgs {
   float renorm_blend; /* the reference's FLASHNEXT_RENORM_BLEND; 1 = plain renorm */
 } VmRouterArgs;
 
-/* vm_moe_layer: the whole decode layer (tokens <= VM_LAYER_MAX_TOKENS):
- * router top-k, device-side expert -> pool slot resolution through
- * slot_table, the shared expert (gate/up/SwiGLU/down) and its sigmoid gate,
- * the routed experts, and the fused combine
+/* vm_moe_layer: one whole MoE layer: router top-k, device-side expert -> pool
+ * slot resolution through slot_table, the shared expert (gate/up/SwiGLU/down)
+ * and its sigmoid gate, the routed experts, and the combine.
+ * tokens <= VM_LAYER_MAX_TOKENS (the reference's custom-kernel bound,
+ * metal_runtime.py:26): decode kernels and the fused combine
  *   y = round(round(sum_j round(down_j) * score_j) + round(sigmoid(g_s) * shared)).
+ * More tokens (bf16): the grouped path (router GEMM, device token-by-expert
+ * sort, MFMA grouped gate/up and down) and the generic combine of
+ * adaptive_topk.py:275-278
+ *   y = round(round(sum_j round(round(down_j) * score_j)) + round(sigmoid(g_s) * shared)).
+ * More tokens in fp32: the decode kernels over chunks of VM_LAYER_MAX_TOKENS.
  * Routed experts come from the pool view (slot_table) or, when slot_table is
  * NULL, from the dense arrays in `gate/up/down` indexed by expert id.
  * shared_inter == 0 means no shared expert. */
@@ -190,13 +196,17 @@ typedef struct VmLayerArgs {
 #define VM_PHASE_ROUTER 1u
 #define VM_PHASE_EXPERTS 2u
 
-/* vm_moe_grouped: the batched/prefill path for any token count.  Token-by-
- * expert sort (histogram -> scan -> scatter) on the device, then per-expert
- * grouped gate/up/SwiGLU and down over each expert's rows, then the combine.
+/* vm_moe_grouped: the expert block of the grouped path for any token count
+ * with given routes (SwitchGLU over expert ids, expert_cache.py:1949-2037):
+ * token-by-expert sort on the device, MFMA grouped gate/up/SwiGLU and down
+ * over every expert's rows, then the combine (bf16 activations).
  * combine_mode 0: fused form (fp32 sum of round(down)*score, as vm_moe_layer)
  * combine_mode 1: generic form of adaptive_topk.py:275-278,
  *   y = round(round(sum_j round(round(down_j) * score_j)) + shared_y)
- * Routes are expert ids resolved through slot_table, or dense indices. */
+ * combine_mode 2: no combine; output [tokens, top_k, hidden] = round(down_j)
+ *   (SwitchGLU without scores, the reference's rows > 8 return shape).
+ * Routes are expert ids resolved through slot_table, or dense indices.  An id
+ * outside 0..expert_count-1 contributes nothing and sets status bit 2. */
 typedef struct VmGroupedArgs {
   const void* x;                 /* [tokens, hidden] */
   const int32_t* inds;           /* [tokens, top_k] expert ids */
@@ -225,7 +235,7 @@ int vm_moe_execute(const VmMoeArgs* args, void* stream);
 uint64_t vm_router_workspace(uint32_t tokens, uint32_t expert_count);
 int vm_router_topk(const VmRouterArgs* args, void* stream);
 
-uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t inter_size,
+uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
                                 uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype);
 int vm_moe_layer(const VmLayerArgs* args, void* stream);
 

@@ -129,6 +129,18 @@ def q4_project(x, packed, scales_bits, biases_bits, group_size=GROUP_SIZE) -> np
     return (qsum * s[None] + xsum[:, None, :] * b[None]).sum(axis=-1)
 
 
+def qmm_project(x, packed, scales_bits, biases_bits, group_size=GROUP_SIZE, weight_mode="bf16") -> np.ndarray:
+    """Matrix form of the projection used for more than 8 rows.
+
+    The reference runs those rows through ``mx.gather_qmm`` (expert_cache.py:
+    806-829; MLX 0.32.2, uv.lock:655), whose matrix kernels dequantise a tile
+    of weights into threadgroup memory in the activation type before the
+    multiply.  Restated: ``w = round(scale*q + bias)`` once per weight (bf16
+    mode), then ``x @ w.T`` accumulated in float64.  Returns float64 [n, out]."""
+    w = _round(dequantize(packed, scales_bits, biases_bits, group_size), weight_mode)
+    return np.asarray(x, dtype=np.float64) @ np.asarray(w, dtype=np.float64).T
+
+
 # --------------------------------------------------------------------------
 # Activations.
 
@@ -219,12 +231,17 @@ def route(x, router_bits, k, mode, logit_bias=None, blend=1.0):
 # Experts and combine.
 
 
-def expert_forward(x, gate, up, down, mode, group_size=GROUP_SIZE):
-    """One expert on rows x: (gate_out, up_out, act, down_out), each rounded."""
-    g = _round(q4_project(x, *gate, group_size=group_size), mode)
-    u = _round(q4_project(x, *up, group_size=group_size), mode)
+def expert_forward(x, gate, up, down, mode, group_size=GROUP_SIZE, qmm=False):
+    """One expert on rows x: (gate_out, up_out, act, down_out), each rounded.
+    ``qmm`` selects the matrix form (weights rounded to the activation type)."""
+    if qmm:
+        project = lambda rows, proj: qmm_project(rows, *proj, group_size=group_size, weight_mode=mode)  # noqa: E731
+    else:
+        project = lambda rows, proj: q4_project(rows, *proj, group_size=group_size)  # noqa: E731
+    g = _round(project(x, gate), mode)
+    u = _round(project(x, up), mode)
     a = swiglu(g, u, mode)
-    d = _round(q4_project(a, *down, group_size=group_size), mode)
+    d = _round(project(a, down), mode)
     return g, u, a, d
 
 
@@ -295,7 +312,7 @@ def generic_combine(down_out, scores, mode, shared_term=None):
 
 
 def execute(x, routes, projections, mode, scores=None, shared_y=None, shared=None,
-            shared_gate=None, group_size=GROUP_SIZE, activation=None):
+            shared_gate=None, group_size=GROUP_SIZE, activation=None, qmm=False):
     """MetalMoEExecutor.execute semantics on dense projections.
 
     routes [T,k] are expert indices into the dense arrays.  Returns
@@ -316,7 +333,7 @@ def execute(x, routes, projections, mode, scores=None, shared_y=None, shared=Non
             e = int(routes[t, j])
             if activation is None:
                 g, u, a, d = expert_forward(x[t:t + 1], _take_expert(gate, e), _take_expert(up, e),
-                                            _take_expert(down, e), mode, group_size)
+                                            _take_expert(down, e), mode, group_size, qmm)
                 g_out[t, j], u_out[t, j], act[t, j] = g[0], u[0], a[0]
             else:
                 a = np.asarray(activation, np.float32)[t, j][None]
@@ -333,29 +350,33 @@ def execute(x, routes, projections, mode, scores=None, shared_y=None, shared=Non
 # The whole layer (adaptive_topk._moe_call at threshold 1.0).
 
 
-def shared_expert(x, layer, mode, group_size=GROUP_SIZE):
+def shared_expert(x, layer, mode, group_size=GROUP_SIZE, qmm=False):
     """(shared [T,H], shared_gate [T,1]) for the layer's shared expert, or (None, None)."""
     if layer.get("shared_gate_proj") is None:
         return None, None
     sg = _take_expert(layer["shared_gate_proj"], 0)
     su = _take_expert(layer["shared_up_proj"], 0)
     sd = _take_expert(layer["shared_down_proj"], 0)
-    _, _, _, shared = expert_forward(x, sg, su, sd, mode, group_size)
+    _, _, _, shared = expert_forward(x, sg, su, sd, mode, group_size, qmm)
     seg = _take_expert(layer["shared_expert_gate"], 0)
     logit = _round(q4_project(x, *seg, group_size=group_size), mode)
     return shared, sigmoid(logit, mode)
 
 
-def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE):
+def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None):
     """One MoE layer.  ``layer`` holds numpy arrays (see veymoe.synth).
 
-    path "decode": rows <= 8, fused shared_y combine (adaptive_topk.py:289-293);
-    path "prefill": generic combine (adaptive_topk.py:275-278).
+    path "decode": rows <= 8, fused shared_y combine (adaptive_topk.py:289-293),
+    vector-form projections;
+    path "prefill": generic combine (adaptive_topk.py:275-278), matrix-form
+    projections (gather_qmm, weights rounded) unless ``qmm`` says otherwise.
     Returns dict(inds, scores, gates, output, down, shared, shared_gate)."""
     x = np.asarray(x, dtype=np.float32)
+    if qmm is None:
+        qmm = path != "decode"
     k = int(layer["top_k"])
     inds, scores, gates = route(x, layer["router"], k, mode, layer.get("router_bias"))
-    shared, shared_gate = shared_expert(x, layer, mode, group_size)
+    shared, shared_gate = shared_expert(x, layer, mode, group_size, qmm)
     projections = {name: layer[name] for name in ("gate_proj", "up_proj", "down_proj")}
     tokens = x.shape[0]
     hidden = x.shape[1]
@@ -364,7 +385,7 @@ def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE):
         rows, cols = np.nonzero(inds == e)
         _, _, _, d = expert_forward(x[rows], _take_expert(projections["gate_proj"], e),
                                     _take_expert(projections["up_proj"], e),
-                                    _take_expert(projections["down_proj"], e), mode, group_size)
+                                    _take_expert(projections["down_proj"], e), mode, group_size, qmm)
         down[rows, cols] = d
     shared_y = None
     if shared is not None:

@@ -9,6 +9,10 @@ summing ``value*q`` and ``value`` over its 32 inputs, then
 ``result += scale*qsum; result += bias*xsum``.  It exists to pin the vectorised
 ``moe_oracle.q4_project`` on tiny shapes, with an independent nibble decode
 (plain integer shifts on Python ints).
+
+``qmm_loops`` restates the matrix form used for more than 8 rows (weights
+dequantised and rounded to bf16 before the multiply) with its own bf16
+rounding on the float32 bit pattern, to pin ``moe_oracle.qmm_project``.
 """
 from __future__ import annotations
 
@@ -51,6 +55,38 @@ def projection_loops(x, routes, weight, scales, biases, output_width, slot_input
                 rows.append(result)
             token_out.append(rows)
         out.append(token_out)
+    return out
+
+
+def _round_bf16_value(value: float) -> float:
+    """float32(value) rounded to bf16, nearest-even, by integer arithmetic on
+    the float32 bit pattern (an independent restatement of the rounding)."""
+    bits = struct.unpack("<I", struct.pack("<f", value))[0]
+    if (bits & 0x7F800000) == 0x7F800000:
+        return struct.unpack("<f", struct.pack("<I", bits & 0xFFFF0000))[0]
+    lower = bits & 0xFFFF
+    upper = bits >> 16
+    if lower > 0x8000 or (lower == 0x8000 and (upper & 1)):
+        upper += 1
+    return struct.unpack("<f", struct.pack("<I", (upper & 0xFFFF) << 16))[0]
+
+
+def qmm_loops(x, weight, scales, biases, group_size=32):
+    """Matrix form for one expert on rows x [n][in]: every weight dequantised
+    as float32(scale*q + bias) rounded to bf16, then plain dot products.
+    weight: [out][in/8] ints; scales/biases [out][in/group] bf16 bits."""
+    out = []
+    for row_x in x:
+        row_out = []
+        for row in range(len(weight)):
+            acc = 0.0
+            for k in range(len(row_x)):
+                q = (int(weight[row][k // 8]) >> ((k & 7) * 4)) & 15
+                group = k // group_size
+                w = _bf16_value(scales[row][group]) * q + _bf16_value(biases[row][group])
+                acc += float(row_x[k]) * _round_bf16_value(w)
+            row_out.append(acc)
+        out.append(row_out)
     return out
 
 

@@ -271,3 +271,43 @@ def test_layer_decode_is_composition_of_parts():
     shared, sg = mo.shared_expert(x, layer, "bf16")
     *_, fused = mo.execute(x, inds, projections, "bf16", scores=scores, shared_y=mo.bf16r(sg * shared))
     np.testing.assert_array_equal(out["output"], fused)
+
+
+def test_qmm_projection_matches_loops():
+    rng = np.random.default_rng(7)
+    out_w, in_w = 5, 64
+    q = rng.integers(0, 16, (out_w, in_w))
+    w = np.array([ref_loops.pack_nibbles(r) for r in q], dtype=np.uint32)
+    s = mo.f32_to_bf16_bits(rng.uniform(0.005, 0.02, (out_w, in_w // 32)).astype(np.float32))
+    b = mo.f32_to_bf16_bits(rng.uniform(-0.1, 0.1, (out_w, in_w // 32)).astype(np.float32))
+    x = mo.bf16r(rng.normal(size=(3, in_w)).astype(np.float32))
+    got = mo.qmm_project(x, w, s, b)
+    want = np.array(ref_loops.qmm_loops(x.tolist(), w.tolist(), s.tolist(), b.tolist()))
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_projection_equals_vector_form_for_exact_weights():
+    """scale 2^-6 and bias -2^-3: every scale*q + bias is exact in bf16, so
+    rounding the weights changes nothing."""
+    rng = np.random.default_rng(8)
+    q = rng.integers(0, 16, (4, 96))
+    w = np.array([ref_loops.pack_nibbles(r) for r in q], dtype=np.uint32)
+    s = mo.f32_to_bf16_bits(np.full((4, 3), 2.0 ** -6, np.float32))
+    b = mo.f32_to_bf16_bits(np.full((4, 3), -0.125, np.float32))
+    x = rng.normal(size=(2, 96))
+    np.testing.assert_allclose(mo.qmm_project(x, w, s, b), mo.q4_project(x, w, s, b), rtol=1e-12, atol=1e-12)
+
+
+def test_qmm_projection_within_weight_rounding_bound():
+    """|qmm - q4| <= sum |x| * half a bf16 step of |w| (2^-9 relative)."""
+    rng = np.random.default_rng(9)
+    q = rng.integers(0, 16, (6, 128))
+    w = np.array([ref_loops.pack_nibbles(r) for r in q], dtype=np.uint32)
+    s = mo.f32_to_bf16_bits(rng.uniform(0.005, 0.02, (6, 4)).astype(np.float32))
+    b = mo.f32_to_bf16_bits(rng.uniform(-0.1, 0.1, (6, 4)).astype(np.float32))
+    x = rng.normal(size=(5, 128))
+    dense = mo.dequantize(w, s, b)
+    bound = np.abs(x) @ (np.abs(dense) * 2.0 ** -8).T
+    diff = np.abs(mo.qmm_project(x, w, s, b) - mo.q4_project(x, w, s, b))
+    assert (diff <= bound + 1e-12).all()
+    assert diff.max() > 0          # the rounding is really applied

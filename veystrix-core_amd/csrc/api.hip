@@ -358,18 +358,61 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   return w;
 }
 
-uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t inter_size, uint32_t shared_inter,
-                                uint32_t expert_count, uint32_t act_dtype) {
-  return layer_ws(tokens, top_k, inter_size, shared_inter, expert_count, act_dtype).total;
+// Workspace of the grouped path (more than VM_LAYER_MAX_TOKENS rows).
+struct GroupedWs {
+  uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, row_token, pair_row, act, rows, total;
+  uint32_t rows_total, groups, max_tiles;
+};
+
+static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint32_t E, bool shared) {
+  GroupedWs w{};
+  w.rows_total = T * K + (shared ? T : 0);
+  w.groups = E + (shared ? 1 : 0);
+  w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups);
+  uint64_t o = kAlign;
+  auto take = [&](uint64_t bytes) {
+    const uint64_t at = o;
+    o += align_up(bytes);
+    return at;
+  };
+  w.logits = take(uint64_t(T) * E * 4);
+  w.sig = take(uint64_t(T) * 2);
+  w.inds = take(uint64_t(T) * K * 4);
+  w.scores = take(uint64_t(T) * K * 2);
+  w.row_off = take(uint64_t(w.groups + 1) * 4);
+  w.tiles = take(uint64_t(w.max_tiles) * 8);
+  w.tile_count = take(4);
+  w.row_token = take(uint64_t(w.rows_total) * 4);
+  w.pair_row = take(uint64_t(T) * K * 4);
+  w.act = take(uint64_t(w.rows_total) * I * 2);
+  w.rows = take(uint64_t(w.rows_total) * H * 2);
+  w.total = o;
+  return w;
 }
+
+static bool use_grouped(uint32_t T, uint32_t dtype) { return T > VM_LAYER_MAX_TOKENS && dtype == VM_BF16; }
+
+// Up to this many rows the grouped layer keeps the decode router kernel (one
+// router row per wave over every token); above, the router is an MFMA GEMM.
+constexpr uint32_t kFrontMaxTokens = 64;
+
+uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
+                                uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype) {
+  if (use_grouped(tokens, act_dtype))
+    return grouped_ws(tokens, top_k, hidden_size, inter_size, expert_count, shared_inter != 0).total;
+  const uint32_t chunk = tokens < VM_LAYER_MAX_TOKENS ? tokens : VM_LAYER_MAX_TOKENS;
+  return layer_ws(chunk, top_k, inter_size, shared_inter, expert_count, act_dtype).total;
+}
+
+static int layer_decode(const VmLayerArgs* a, hipStream_t stream);
+static int layer_grouped(const VmLayerArgs* a, hipStream_t stream);
 
 int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   if (a == nullptr) return fail(VM_EINVAL, "null arguments");
   const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
-  int rc = validate_router(T, H, E, K, a->act_dtype);
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size;
+  int rc = validate_router(T, H, a->expert_count, K, a->act_dtype);
   if (rc != VM_OK) return rc;
-  if (T > VM_LAYER_MAX_TOKENS) return fail(VM_EINVAL, "tokens must be in 1..%u", VM_LAYER_MAX_TOKENS);
   if (a->group_size != 32) return fail(VM_EUNSUPPORTED, "group_size must be 32");
   if (I == 0 || I % 32) return fail(VM_EINVAL, "Q4/G32 projection inputs must be group aligned");
   if (a->shared_inter != 0 && a->shared_inter != I)
@@ -392,6 +435,30 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   }
   rc = check_pool(a->pool, H, I);
   if (rc != VM_OK) return rc;
+  const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
+  if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  if (use_grouped(T, a->act_dtype)) return layer_grouped(a, stream);
+  if (T <= VM_LAYER_MAX_TOKENS) return layer_decode(a, stream);
+  // fp32 activations above the decode bound: decode kernels in chunks of
+  // VM_LAYER_MAX_TOKENS tokens (with no rounding the fused and the generic
+  // combine agree)
+  for (uint32_t t0 = 0; t0 < T; t0 += VM_LAYER_MAX_TOKENS) {
+    VmLayerArgs c = *a;
+    const uint32_t n = T - t0 < VM_LAYER_MAX_TOKENS ? T - t0 : VM_LAYER_MAX_TOKENS;
+    c.tokens = n;
+    c.x = static_cast<const float*>(a->x) + uint64_t(t0) * H;
+    c.output = static_cast<float*>(a->output) + uint64_t(t0) * H;
+    if (a->inds_out != nullptr) c.inds_out = a->inds_out + uint64_t(t0) * K;
+    if (a->scores_out != nullptr) c.scores_out = static_cast<float*>(a->scores_out) + uint64_t(t0) * K;
+    rc = layer_decode(&c, stream);
+    if (rc != VM_OK) return rc;
+  }
+  return VM_OK;
+}
+
+static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
+  const bool shared = a->shared_inter != 0;
   const uint32_t S = K + (shared ? 1 : 0);
   if (!vm::gateup_supported(H)) return fail(VM_EUNSUPPORTED, "hidden_size %u is above the decode kernel bound", H);
   if (!vm::down_supported(I, S, a->act_dtype)) return fail(VM_EUNSUPPORTED, "inter_size %u is above the decode kernel bound", I);
@@ -404,7 +471,6 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   uint32_t* words = reinterpret_cast<uint32_t*>(ws + w.words);
   float* logits = reinterpret_cast<float*>(ws + w.logits);
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
-  if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
   // fused: the gate/up blocks select the experts themselves from the logits;
   // split: a select kernel publishes inds/scores for the host between phases
   const bool fused = phases == (VM_PHASE_ROUTER | VM_PHASE_EXPERTS);
@@ -492,6 +558,240 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   return VM_OK;
 }
 
+
+// The experts of the grouped path: sort the routes, gate/up + SwiGLU and down
+// over every group's rows, combine.  `sig`/shared projections are used when
+// `shared` is set (the layer's own shared expert).
+struct GroupedExperts {
+  const void* x;
+  const int32_t* inds;
+  const void* scores;
+  VmQ4Proj gate, up, down;
+  VmPoolView pool;
+  const int32_t* slot_table;
+  bool shared;
+  VmQ4Proj shared_gate, shared_up, shared_down;
+  const void* sig;
+  const void* shared_y;
+  void* output;
+  uint32_t* status;
+  uint32_t T, K, H, I, E;
+  int mode;
+};
+
+static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char* ws, hipStream_t stream) {
+  vm::SortLaunch s{};
+  s.inds = g.inds;
+  s.row_off = reinterpret_cast<uint32_t*>(ws + w.row_off);
+  s.tiles = reinterpret_cast<uint2*>(ws + w.tiles);
+  s.tile_count = reinterpret_cast<uint32_t*>(ws + w.tile_count);
+  s.row_token = reinterpret_cast<uint32_t*>(ws + w.row_token);
+  s.pair_row = reinterpret_cast<uint32_t*>(ws + w.pair_row);
+  s.status = g.status;
+  s.tokens = g.T;
+  s.slots = g.K;
+  s.experts = g.E;
+  s.shared_rows = g.shared ? g.T : 0;
+  hipError_t e = vm::launch_sort(s, stream);
+  if (e != hipSuccess) return hip_fail(e, "sort launch");
+
+  vm::GroupedLaunch q{};
+  q.row_off = s.row_off;
+  q.tiles = s.tiles;
+  q.tile_count = s.tile_count;
+  q.slot_table = g.slot_table;
+  q.pool = to_pool(g.pool);
+  q.status = g.status;
+  q.experts = g.E;
+  // gate/up + SwiGLU over the gathered token rows
+  q.a = static_cast<const uint16_t*>(g.x);
+  q.row_token = s.row_token;
+  q.dense[0] = to_ptrs(g.gate);
+  q.dense[1] = to_ptrs(g.up);
+  if (g.shared) {
+    q.shared[0] = to_ptrs(g.shared_gate);
+    q.shared[1] = to_ptrs(g.shared_up);
+  }
+  q.part[0] = 0;
+  q.part[1] = 1;
+  q.out = ws + w.act;
+  q.k_dim = g.H;
+  q.n_dim = g.I;
+  q.a_stride = g.H;
+  e = vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
+  if (e != hipSuccess) return hip_fail(e, "grouped gate/up launch");
+  // down over the contiguous activation rows
+  q.a = reinterpret_cast<const uint16_t*>(ws + w.act);
+  q.row_token = nullptr;
+  q.dense[0] = to_ptrs(g.down);
+  q.dense[1] = vm::ProjPtrs{};
+  q.shared[0] = g.shared ? to_ptrs(g.shared_down) : vm::ProjPtrs{};
+  q.shared[1] = vm::ProjPtrs{};
+  q.part[0] = 2;
+  q.out = ws + w.rows;
+  q.k_dim = g.I;
+  q.n_dim = g.H;
+  q.a_stride = g.I;
+  e = vm::launch_grouped(vm::kEpiRows, q, w.max_tiles, stream);
+  if (e != hipSuccess) return hip_fail(e, "grouped down launch");
+
+  vm::CombineLaunch c{};
+  c.rows = reinterpret_cast<const uint16_t*>(ws + w.rows);
+  c.pair_row = s.pair_row;
+  c.scores = g.scores;
+  c.score_dtype = VM_BF16;
+  if (g.shared) {
+    c.shared_first = s.row_off + g.E;
+    c.shared_sig = g.sig;
+  }
+  c.shared_y = g.shared_y;
+  c.out = g.output;
+  c.tokens = g.T;
+  c.slots = g.K;
+  c.hidden = g.H;
+  c.mode = g.mode;
+  e = vm::launch_grouped_combine(c, stream);
+  if (e != hipSuccess) return hip_fail(e, "combine launch");
+  return VM_OK;
+}
+
+static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
+  const bool shared = a->shared_inter != 0;
+  const GroupedWs w = grouped_ws(T, K, H, I, E, shared);
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
+  if (!aligned16(a->output)) return fail(VM_EINVAL, "output must be 16-byte aligned");
+  char* ws = static_cast<char*>(a->workspace);
+  int32_t* inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
+  void* scores = a->scores_out != nullptr ? a->scores_out : static_cast<void*>(ws + w.scores);
+  uint16_t* sig = reinterpret_cast<uint16_t*>(ws + w.sig);
+  const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
+  hipError_t e = hipSuccess;
+  if ((phases & VM_PHASE_ROUTER) && T <= kFrontMaxTokens) {
+    // few rows: the decode router (one row per wave, every token) and shared gate
+    vm::FrontLaunch f{};
+    f.x = a->x;
+    f.weight = a->router_weight;
+    f.bias = a->router_bias;
+    f.logits = reinterpret_cast<float*>(ws + w.logits);
+    if (shared) f.seg = to_ptrs(a->shared_expert_gate);
+    f.shared_sig = sig;
+    f.tokens = T;
+    f.hidden = H;
+    f.experts = E;
+    f.act_dtype = VM_BF16;
+    e = vm::launch_front(f, stream);
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+  } else if (phases & VM_PHASE_ROUTER) {
+    // router logits as an MFMA GEMM over all rows
+    vm::GroupedLaunch r{};
+    r.a = static_cast<const uint16_t*>(a->x);
+    r.rows = T;
+    r.bf16_weight = a->router_weight;
+    r.bias = a->router_bias;
+    r.out = ws + w.logits;
+    r.k_dim = H;
+    r.n_dim = E;
+    r.a_stride = H;
+    r.experts = E;
+    e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRows - 1) / vm::kGroupedRows, stream);
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    if (shared) {
+      e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T, H,
+                                 stream);
+      if (e != hipSuccess) return hip_fail(e, "shared gate launch");
+    }
+  }
+  if (phases & VM_PHASE_ROUTER) {
+    // softmax / top-k / renorm per row
+    vm::SelectLaunch s{};
+    s.logits = reinterpret_cast<const float*>(ws + w.logits);
+    s.inds = inds;
+    s.scores = scores;
+    s.tokens = T;
+    s.experts = E;
+    s.top_k = K;
+    s.act_dtype = VM_BF16;
+    s.blend = a->renorm_blend;
+    e = vm::launch_select(s, stream);
+    if (e != hipSuccess) return hip_fail(e, "select launch");
+  }
+  if (!(phases & VM_PHASE_EXPERTS)) return VM_OK;
+  GroupedExperts g{};
+  g.x = a->x;
+  g.inds = inds;
+  g.scores = scores;
+  g.gate = a->gate;
+  g.up = a->up;
+  g.down = a->down;
+  g.pool = a->pool;
+  g.slot_table = a->slot_table;
+  g.shared = shared;
+  g.shared_gate = a->shared_gate_proj;
+  g.shared_up = a->shared_up_proj;
+  g.shared_down = a->shared_down_proj;
+  g.sig = sig;
+  g.output = a->output;
+  g.status = a->status;
+  g.T = T;
+  g.K = K;
+  g.H = H;
+  g.I = I;
+  g.E = E;
+  g.mode = 1;  // rows > 8: the reference's generic combine
+  return run_grouped_experts(g, w, ws, stream);
+}
+
+uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
+                                  uint32_t expert_count, uint32_t act_dtype) {
+  (void)act_dtype;
+  return grouped_ws(tokens, top_k, hidden_size, inter_size, expert_count, false).total;
+}
+
+int vm_moe_grouped(const VmGroupedArgs* a, void* stream_ptr) {
+  if (a == nullptr) return fail(VM_EINVAL, "null arguments");
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
+  if (a->act_dtype != VM_BF16) return fail(VM_EUNSUPPORTED, "the grouped kernels take bf16 activations");
+  if (T == 0 || K == 0 || K > kMaxTopK) return fail(VM_EINVAL, "tokens must be positive and top_k in 1..%u", kMaxTopK);
+  if (E == 0 || E > kMaxExperts) return fail(VM_EINVAL, "expert_count must be in 1..%u", kMaxExperts);
+  if (H == 0 || H % 32 || I == 0 || I % 32) return fail(VM_EINVAL, "hidden_size and inter_size must be multiples of 32");
+  if (a->group_size != 32) return fail(VM_EUNSUPPORTED, "group_size must be 32");
+  if (a->combine_mode > 2) return fail(VM_EINVAL, "combine_mode must be 0, 1 or 2");
+  if (a->x == nullptr || a->inds == nullptr || a->output == nullptr)
+    return fail(VM_EINVAL, "x, inds and output are required");
+  if (a->combine_mode != 2 && a->scores == nullptr) return fail(VM_EINVAL, "scores are required to combine");
+  if (!aligned16(a->x) || !aligned16(a->output) || (a->shared_y != nullptr && !aligned16(a->shared_y)))
+    return fail(VM_EINVAL, "x, output and shared_y must be 16-byte aligned");
+  if (a->slot_table != nullptr && a->pool.base == nullptr) return fail(VM_EINVAL, "a slot table needs a pool view");
+  if (a->slot_table == nullptr && a->gate.weight == nullptr && a->pool.base == nullptr)
+    return fail(VM_EINVAL, "experts need a slot table with a pool view, or dense projections");
+  if (!proj_ok(a->gate) || !proj_ok(a->up) || !proj_ok(a->down)) return fail(VM_EINVAL, "malformed projection");
+  int rc = check_pool(a->pool, H, I);
+  if (rc != VM_OK) return rc;
+  const GroupedWs w = grouped_ws(T, K, H, I, E, false);
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
+  GroupedExperts g{};
+  g.x = a->x;
+  g.inds = a->inds;
+  g.scores = a->scores;
+  g.gate = a->gate;
+  g.up = a->up;
+  g.down = a->down;
+  g.pool = a->pool;
+  g.slot_table = a->slot_table;
+  g.shared_y = a->shared_y;
+  g.output = a->output;
+  g.status = a->status;
+  g.T = T;
+  g.K = K;
+  g.H = H;
+  g.I = I;
+  g.E = E;
+  g.mode = static_cast<int>(a->combine_mode);
+  return run_grouped_experts(g, w, static_cast<char*>(a->workspace), static_cast<hipStream_t>(stream_ptr));
+}
 
 // ------------------------------------------------------------ combine ---
 

@@ -1,20 +1,543 @@
-// Batched decode / chunked prefill path (token-by-expert grouping).
+// Grouped (token-by-expert) kernels of the MoE layer for gfx950: the batched
+// decode and chunked prefill path (more than 8 rows).
+//
+//   sort     count the (token, slot) pairs of every expert with atomics, one
+//            block scans the counts into row offsets and a tile list, then the
+//            pairs are scattered into expert order (row -> token, pair ->
+//            row).  The rows of one expert are contiguous; their order inside
+//            the expert changes no result, since every output row is its own
+//            set of dot products.  The shared expert is one more group whose
+//            rows are all the tokens.
+//   gemm     one workgroup per (tile of <= 64 rows of one group, tile of output
+//            features).  K runs in chunks of eight 32-input groups: the A rows
+//            are staged in LDS (double buffered, pair-permuted to match the
+//            dequantised weights), each lane dequantises one 16-byte Q4 group
+//            per chunk and projection into bf16 (f16 magic number + v_fma_mix
+//            + v_cvt_pk_bf16_f32) and feeds v_mfma_f32_16x16x32_bf16 with fp32
+//            accumulation.  Epilogues: SwiGLU of gate and up, bf16 rows (down),
+//            router logits (bf16 weights).
+//   combine  per token, the expert rows in slot order with the router scores
+//            and the shared term.
+//
+// MFMA operand layout (v_mfma_f32_16x16x32_bf16): lane l supplies 8 bf16 of A
+// row l%16 and 8 bf16 of B column l%16, both for the k block l/16; it receives
+// C[4*(l/16) + i][l%16], i < 4.  Chunk step st feeds k block kb from group
+// g0 + 4*(st/4) + kb, packed word st%4 (8 inputs), so eight steps cover the
+// chunk's eight groups and a lane's weight loads are whole 16-byte groups.
+
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
-#include "../../include/veymoe.h"
 #include "vm_internal.h"
 
-extern "C" {
+namespace vm {
 
-uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
-                                  uint32_t expert_count, uint32_t act_dtype) {
-  (void)tokens; (void)top_k; (void)hidden_size; (void)inter_size; (void)expert_count; (void)act_dtype;
-  return 0;
+namespace {
+
+constexpr int kGB = 256;                 // threads per block of the small kernels
+constexpr int kBM = kGroupedRows;        // rows per tile
+constexpr int kMB = kBM / 16;            // MFMA row blocks
+constexpr int kCG = 8;                   // 32-input groups per K chunk (a 128-byte line per weight row)
+constexpr int kHalves = kCG / 4;         // groups per lane and chunk
+constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
+constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
+constexpr int kStageBytes = kBM * kRowBytes;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ uint4 g_zero_page[64];  // lanes without data load zeros from here
+
+__device__ __forceinline__ void flag(uint32_t* status, uint32_t bits) {
+  if (status != nullptr) atomicOr(status, bits);
 }
 
-int vm_moe_grouped(const VmGroupedArgs* a, void* stream) {
-  (void)a; (void)stream;
-  return VM_EUNSUPPORTED;
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-}  // extern "C"
+// 8 inputs of one packed word -> bf16 pairs (q_n, q_{n+4}) for n < 4, the
+// order pair_activations gives the activations.  (1024 + q) is exact in f16;
+// s * (1024 + q) + (b - 1024 s) is one fp32 fma per value.
+__device__ __forceinline__ void dequant_word(uint32_t word, float s, float b1024, uint32_t out[4]) {
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    const uint32_t m = ((word >> (4 * n)) & 0x000F000Fu) | 0x64006400u;
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, m);
+    out[n] = pack_bf16(fmaf(s, static_cast<float>(h.x), b1024), fmaf(s, static_cast<float>(h.y), b1024));
+  }
+}
+
+// bf16 weights: natural pairs (k0 k1)(k2 k3)(k4 k5)(k6 k7) -> (k0 k4)(k1 k5)(k2 k6)(k3 k7)
+__device__ __forceinline__ void permute_word(const uint4 v, uint32_t out[4]) {
+  out[0] = (v.x & 0xffffu) | (v.z << 16);
+  out[1] = (v.x >> 16) | (v.z & 0xffff0000u);
+  out[2] = (v.y & 0xffffu) | (v.w << 16);
+  out[3] = (v.y >> 16) | (v.w & 0xffff0000u);
+}
+
+__device__ __forceinline__ bf16x8_t as_operand(const uint32_t r[4]) {
+  const uint4 v = make_uint4(r[0], r[1], r[2], r[3]);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+// ------------------------------------------------------------------ gemm ---
+
+// B side of one lane for one chunk: groups g0 + 4 h + kb (h < kHalves) of
+// one weight row, Q4 (16 bytes + scale + bias each) or bf16 (32 weights each).
+// Chunk step st uses half st/4, packed word st%4.
+template <bool Q4>
+struct BChunk;
+
+template <>
+struct BChunk<true> {
+  uint4 w[kHalves];
+  uint32_t s[kHalves], b[kHalves];
+  __device__ __forceinline__ void load(const ProjPtrs& p, bool live, size_t row, uint32_t g0, uint32_t kb,
+                                       uint32_t K) {
+    const uint32_t G = K / kGroup;
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) {
+      const uint32_t g = g0 + 4 * h + kb;
+      const bool l = live && g < G;
+      const size_t wo = row * (K / 8) + g * kWordsPerGroup;
+      const size_t mo = row * G + g;
+      w[h] = ldg16(l ? static_cast<const void*>(p.w + wo) : static_cast<const void*>(g_zero_page));
+      s[h] = ldg_u16(l ? static_cast<const void*>(p.s + mo) : static_cast<const void*>(g_zero_page));
+      b[h] = ldg_u16(l ? static_cast<const void*>(p.b + mo) : static_cast<const void*>(g_zero_page));
+    }
+  }
+  __device__ __forceinline__ bf16x8_t step(int st) const {
+    const int h = st >> 2, i = st & 3;
+    const float sf = bf16_to_f32(s[h]);
+    const float b1024 = fmaf(-1024.0f, sf, bf16_to_f32(b[h]));
+    const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
+    uint32_t r[4];
+    dequant_word(word, sf, b1024, r);
+    return as_operand(r);
+  }
+};
+
+template <>
+struct BChunk<false> {
+  uint4 v[kHalves][4];
+  __device__ __forceinline__ void load(const uint16_t* wbf, bool live, size_t row, uint32_t g0, uint32_t kb,
+                                       uint32_t K) {
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) {
+      const uint32_t g = g0 + 4 * h + kb;
+      const bool l = live && g < K / kGroup;
+      const uint16_t* src = l ? wbf + row * K + g * kGroup : reinterpret_cast<const uint16_t*>(g_zero_page);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 8 * i);
+    }
+  }
+  __device__ __forceinline__ bf16x8_t step(int st) const {
+    uint32_t r[4];
+    permute_word(v[st >> 2][st & 3], r);
+    return as_operand(r);
+  }
+};
+
+// EPI: 0 SwiGLU of projections 0 (gate) and 1 (up) -> bf16 [rows, N];
+//      1 bf16 rows -> [rows, N]; 2 router logits (bf16 weights) -> fp32 [rows, N].
+template <int EPI, int WAVES, int NBW, int PROJ>
+__global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
+  static_assert(WAVES >= 4, "the A staging uses the first 256 threads");
+  constexpr bool Q4 = EPI != kEpiLogits;
+  constexpr int kThreads = WAVES * 64;
+  constexpr int kItems = kBM * kCG / kThreads;  // A staging items per thread
+  extern __shared__ uint4 s_dyn[];               // two A stages of kStageBytes
+  uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
+
+  const uint32_t tid = threadIdx.x;
+  const uint32_t lane = tid & 63u;
+  const uint32_t wave = tid >> 6;
+
+  // the tile: rows [row0, row0 + rows) of `group`
+  uint32_t group = 0, row0, rows;
+  if (p.tiles != nullptr) {
+    if (blockIdx.y >= *p.tile_count) return;
+    const uint2 td = p.tiles[blockIdx.y];
+    group = td.x;
+    row0 = p.row_off[group] + td.y;
+    rows = min(p.row_off[group + 1] - row0, static_cast<uint32_t>(kBM));
+  } else {
+    row0 = blockIdx.y * kBM;
+    if (row0 >= p.rows) return;
+    rows = min(p.rows - row0, static_cast<uint32_t>(kBM));
+  }
+  const uint32_t K = p.k_dim, N = p.n_dim, G = K / kGroup;
+  const uint32_t n_wave = (blockIdx.x * WAVES + wave) * NBW * 16;
+
+  // the group's weights
+  ProjPtrs w[PROJ];
+  bool ok = true;
+  if constexpr (Q4) {
+    if (group >= p.experts) {
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) w[pj] = p.shared[pj];
+      ok = w[0].w != nullptr;
+    } else {
+      uint32_t index = 0;
+      const int kind = resolve_word(group, p.slot_table, p.experts, p.pool, &p.stream, p.dense[0].w != nullptr, index);
+      ok = kind != kSrcNone;
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
+    }
+    if (!ok && tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
+  }
+
+  // A staging: item it = tid + j * threads -> (row it / kCG, group it % kCG
+  // of the chunk), 64 bytes each
+  uint32_t a_off[kItems];
+  const uint16_t* a_src[kItems];
+  bool a_live_row[kItems];
+  uint32_t a_q[kItems];
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const uint32_t it = tid + j * kThreads;
+    const uint32_t r = it / kCG, q = it % kCG;
+    a_live_row[j] = r < rows;
+    const uint32_t arow = a_live_row[j] ? (p.row_token != nullptr ? p.row_token[row0 + r] : row0 + r) : 0u;
+    a_src[j] = p.a + static_cast<size_t>(arow) * p.a_stride;
+    a_q[j] = q;
+    a_off[j] = r * kRowBytes + q * 64;
+  }
+  uint4 ar[kItems][4];
+  auto a_load = [&](uint32_t g0) {
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      const uint32_t g = g0 + a_q[j];
+      const bool live = a_live_row[j] && g < G;
+      const uint16_t* src = live ? a_src[j] + g * kGroup : reinterpret_cast<const uint16_t*>(g_zero_page);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ar[j][i] = ldg16(src + 8 * i);
+    }
+  };
+  auto a_store = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < kItems; ++j) {
+      uint32_t raw[16], xp[16];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        raw[4 * i] = ar[j][i].x; raw[4 * i + 1] = ar[j][i].y; raw[4 * i + 2] = ar[j][i].z; raw[4 * i + 3] = ar[j][i].w;
+      }
+      pair_activations(raw, xp);
+      uint4* dst = reinterpret_cast<uint4*>(s_a0 + buf * kStageBytes + a_off[j]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(xp[4 * i], xp[4 * i + 1], xp[4 * i + 2], xp[4 * i + 3]);
+    }
+  };
+
+  // B: lane -> (column lane%16 of each block, group g0 + lane/16)
+  const uint32_t bn = lane & 15u, bkb = lane >> 4;
+  BChunk<Q4> bc[PROJ][NBW], bn_next[PROJ][NBW];
+  auto b_load = [&](BChunk<Q4> (&dst)[PROJ][NBW], uint32_t g0) {
+#pragma unroll
+    for (int pj = 0; pj < PROJ; ++pj) {
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        const uint32_t col = n_wave + nb * 16 + bn;
+        const bool live = ok && col < N;
+        if constexpr (Q4) dst[pj][nb].load(w[pj], live, col, g0, bkb, K);
+        else dst[pj][nb].load(p.bf16_weight, live, col, g0, bkb, K);
+      }
+    }
+  };
+
+  f32x4_t acc[PROJ][NBW][kMB];
+#pragma unroll
+  for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) acc[pj][nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  const uint32_t chunks = (G + kCG - 1) / kCG;
+  a_load(0);
+  b_load(bc, 0);
+  a_store(0);
+  __syncthreads();
+  const uint32_t am = lane & 15u, akb = lane >> 4;
+  for (uint32_t c = 0; c < chunks; ++c) {
+    const int buf = c & 1;
+    const bool more = c + 1 < chunks;
+    if (more) {
+      a_load((c + 1) * kCG);
+      b_load(bn_next, (c + 1) * kCG);
+    }
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      bf16x8_t bop[PROJ][NBW];
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) bop[pj][nb] = bc[pj][nb].step(st);
+#pragma unroll
+      for (int mb = 0; mb < kMB; ++mb) {
+        if (static_cast<uint32_t>(mb * 16) >= rows) break;  // block-uniform
+        const uint4 av = *reinterpret_cast<const uint4*>(
+            s_a0 + buf * kStageBytes + (mb * 16 + am) * kRowBytes + ((st >> 2) * 4 + akb) * 64 + (st & 3) * 16);
+        const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, av);
+#pragma unroll
+        for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+          for (int nb = 0; nb < NBW; ++nb)
+            acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[pj][nb], acc[pj][nb][mb], 0, 0, 0);
+      }
+    }
+    if (more) {
+      a_store(buf ^ 1);
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) bc[pj][nb] = bn_next[pj][nb];
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds rows 4*(lane/16) + i of every row block, column lane%16
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    const uint32_t col = n_wave + nb * 16 + bn;
+    if (col >= N) continue;
+#pragma unroll
+    for (int mb = 0; mb < kMB; ++mb) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t r = mb * 16 + 4 * bkb + i;
+        if (r >= rows) continue;
+        const size_t o = static_cast<size_t>(row0 + r) * N + col;
+        if constexpr (EPI == kEpiSwiglu) {
+          const float gv = round_bf16(acc[0][nb][mb][i]);
+          const float uv = round_bf16(acc[PROJ - 1][nb][mb][i]);
+          ActBF16::store(p.out, o, ok ? swiglu_act<ActBF16>(gv, uv) : 0.0f);
+        } else if constexpr (EPI == kEpiRows) {
+          ActBF16::store(p.out, o, round_bf16(acc[0][nb][mb][i]));
+        } else {
+          float v = acc[0][nb][mb][i];
+          if (p.bias != nullptr) v += p.bias[col];
+          static_cast<float*>(p.out)[o] = round_bf16(v);
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ sort ---
+
+// Inclusive scan of one value per thread over a block of 1024 threads.
+__device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
+  const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t u = __shfl_up(v, d, 64);
+    if (lane >= static_cast<uint32_t>(d)) v += u;
+  }
+  if (lane == 63) s_wave[wave] = v;
+  __syncthreads();
+  uint32_t before = 0;
+  for (uint32_t i = 0; i < wave; ++i) before += s_wave[i];
+  __syncthreads();
+  return v + before;
+}
+
+// The whole sort in one block: LDS histogram of the routes, scan into row
+// offsets and the tile list (group, first row) of kBM-row tiles, LDS cursors,
+// scatter.  groups = experts (+1 for the shared rows) <= 1024.
+__global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
+  __shared__ uint32_t s_count[1024];
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_shared_first;
+  const uint32_t g = threadIdx.x;
+  const uint32_t pairs = p.tokens * p.slots;
+  const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
+  s_count[g] = 0;
+  __syncthreads();
+  for (uint32_t i = g; i < pairs; i += 1024) {
+    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
+    if (e < p.experts) atomicAdd(&s_count[e], 1u);
+    else flag(p.status, 2u);
+  }
+  __syncthreads();
+  uint32_t n = 0;
+  if (g < p.experts) n = s_count[g];
+  else if (g < groups) n = p.shared_rows;
+  const uint32_t nt = (n + kBM - 1) / kBM;
+  const uint32_t row_end = block_scan_1024(n, s_wave);
+  const uint32_t tile_end = block_scan_1024(nt, s_wave);
+  const uint32_t row_begin = row_end - n, tile_begin = tile_end - nt;
+  if (g < groups) {
+    p.row_off[g] = row_begin;
+    for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * kBM);
+  }
+  if (g == groups - 1) {
+    p.row_off[groups] = row_end;
+    *p.tile_count = tile_end;
+  }
+  if (g == p.experts) s_shared_first = row_begin;
+  s_count[g] = row_begin;  // scatter cursors
+  __syncthreads();
+  for (uint32_t i = g; i < pairs; i += 1024) {
+    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
+    if (e < p.experts) {
+      const uint32_t pos = atomicAdd(&s_count[e], 1u);
+      p.row_token[pos] = i / p.slots;
+      p.pair_row[i] = pos;
+    } else {
+      p.pair_row[i] = kNoRow;
+    }
+  }
+  for (uint32_t i = g; i < p.shared_rows; i += 1024) p.row_token[s_shared_first + i] = i;
+}
+
+// --------------------------------------------------------------- combine ---
+
+// One thread per 8 outputs of one token.  mode 1 (generic): products rounded,
+// summed in slot order in fp32, rounded; mode 0 (fused): fp32 sum of
+// round(down) * score.  Then + round(sigmoid gate * shared) or + shared_y.
+// mode 2: no combine, out[t, j] = the slot's expert output row.
+__global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
+  const uint32_t per_token = p.hidden / 8;
+  const uint32_t i = blockIdx.x * kGB + threadIdx.x;
+  if (i >= p.tokens * per_token) return;
+  const uint32_t t = i / per_token, h0 = (i % per_token) * 8;
+  if (p.mode == 2) {  // no combine: every slot's rounded expert output
+    for (uint32_t j = 0; j < p.slots; ++j) {
+      const uint32_t row = p.pair_row[t * p.slots + j];
+      const uint4 v = row == kNoRow ? make_uint4(0, 0, 0, 0)
+                                    : ldg16(p.rows + static_cast<size_t>(row) * p.hidden + h0);
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + (static_cast<size_t>(t) * p.slots + j) * p.hidden +
+                                h0) = v;
+    }
+    return;
+  }
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (uint32_t j = 0; j < p.slots; ++j) {
+    const uint32_t row = p.pair_row[t * p.slots + j];
+    if (row == kNoRow) continue;
+    const float sc = load_any(p.scores, static_cast<size_t>(t) * p.slots + j, p.score_dtype);
+    const uint4 v = ldg16(p.rows + static_cast<size_t>(row) * p.hidden + h0);
+    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = bf16_to_f32(e & 1 ? words[e / 2] >> 16 : words[e / 2] & 0xffffu);
+      const float prod = __fmul_rn(d, sc);
+      acc[e] = __fadd_rn(acc[e], p.mode == 1 ? round_bf16(prod) : prod);
+    }
+  }
+  uint32_t out[4];
+  uint4 sh = make_uint4(0, 0, 0, 0);
+  float sig = 0.0f;
+  if (p.shared_first != nullptr) {
+    sh = ldg16(p.rows + (static_cast<size_t>(*p.shared_first) + t) * p.hidden + h0);
+    sig = ActBF16::load(p.shared_sig, t);
+  } else if (p.shared_y != nullptr) {
+    sh = ldg16(static_cast<const uint16_t*>(p.shared_y) + static_cast<size_t>(t) * p.hidden + h0);
+  }
+  const uint32_t shw[4] = {sh.x, sh.y, sh.z, sh.w};
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    float y[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      float v = round_bf16(acc[e + k]);
+      const float s = bf16_to_f32(k ? shw[e / 2] >> 16 : shw[e / 2] & 0xffffu);
+      if (p.shared_first != nullptr) v = round_bf16(__fadd_rn(v, round_bf16(__fmul_rn(sig, s))));
+      else if (p.shared_y != nullptr) v = round_bf16(__fadd_rn(v, s));
+      y[k] = v;
+    }
+    out[e / 2] = f32_to_bf16(y[0]) | (f32_to_bf16(y[1]) << 16);
+  }
+  *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + static_cast<size_t>(t) * p.hidden + h0) =
+      make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+// ----------------------------------------------------------- shared gate ---
+
+// sigmoid(round(x . dequant(seg))) per token, one wave per token (bf16).
+__global__ __launch_bounds__(64) void k_shared_gate(const uint16_t* x, ProjPtrs seg, uint16_t* sig, uint32_t hidden) {
+  const uint32_t t = blockIdx.x, lane = threadIdx.x, G = hidden / kGroup;
+  float acc = 0.0f;
+  for (uint32_t g = lane; g < G; g += 64) {
+    const uint4 w = ldg16(seg.w + g * kWordsPerGroup);
+    const uint16_t* src = x + static_cast<size_t>(t) * hidden + g * kGroup;
+    uint32_t raw[16], xp[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = ldg16(src + 8 * i);
+      raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
+    }
+    pair_activations(raw, xp);
+    const float sum = bf16_pair_sum(raw);
+    acc += fmaf(bf16_to_f32(seg.s[g]), q4_dot_bf16(w, xp) - 128.0f * sum, bf16_to_f32(seg.b[g]) * sum);
+  }
+  const float logit = round_bf16(wave_sum_all(acc));
+  if (lane == 0) ActBF16::store(sig, t, sigmoid_act<ActBF16>(logit));
+}
+
+// ------------------------------------------------------------ dispatch ----
+
+template <class... KArgs, class... Args>
+hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t stream,
+                  Args... args) {
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (timing_events(family, &start, &stop))
+    hipExtLaunchKernelGGL(kernel, grid, block, 0, stream, start, stop, 0, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, args...);
+  return hipGetLastError();
+}
+
+template <int EPI, int WAVES, int NBW, int PROJ>
+hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  constexpr uint32_t lds = 2 * kStageBytes;
+  static bool attr = false;  // one attribute call per kernel instance
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_grouped<EPI, WAVES, NBW, PROJ>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const uint32_t cols = WAVES * NBW * 16;
+  const dim3 grid((p.n_dim + cols - 1) / cols, max_tiles);
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (timing_events(family, &start, &stop))
+    hipExtLaunchKernelGGL((k_grouped<EPI, WAVES, NBW, PROJ>), grid, dim3(WAVES * 64), lds, stream, start, stop, 0, p);
+  else
+    hipLaunchKernelGGL((k_grouped<EPI, WAVES, NBW, PROJ>), grid, dim3(WAVES * 64), lds, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups) { return (rows + kBM - 1) / kBM + groups; }
+
+hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  switch (epi) {
+    case kEpiSwiglu: return grouped_go<kEpiSwiglu, 8, 1, 2>("grouped_gateup", p, max_tiles, stream);
+    case kEpiRows: return grouped_go<kEpiRows, 8, 2, 1>("grouped_down", p, max_tiles, stream);
+    default: return grouped_go<kEpiLogits, 4, 1, 1>("router_gemm", p, max_tiles, stream);
+  }
+}
+
+hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
+  return launch("sort", k_sort, dim3(1), dim3(1024), stream, p);
+}
+
+hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {
+  const uint32_t n = p.tokens * (p.hidden / 8);
+  return launch("combine", k_grouped_combine, dim3((n + kGB - 1) / kGB), dim3(kGB), stream, p);
+}
+
+hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
+                              uint32_t hidden, hipStream_t stream) {
+  return launch("router", k_shared_gate, dim3(tokens), dim3(64), stream, x, seg, sig, hidden);
+}
+
+}  // namespace vm

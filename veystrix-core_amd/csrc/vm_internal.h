@@ -81,6 +81,64 @@ struct DownLaunch {
   int act_dtype;
 };
 
+// ---------------------------------------------------------- grouped path --
+constexpr int kGroupedRows = 64;          // rows per grouped GEMM tile
+constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
+enum : int { kEpiSwiglu = 0, kEpiRows = 1, kEpiLogits = 2 };
+
+// Grouped GEMM over row tiles of expert groups: out[row, n] from A rows x
+// dequantised weights (or bf16 router weights).
+struct GroupedLaunch {
+  const uint16_t* a;           // bf16 activations, a_stride elements per row
+  const uint32_t* row_token;   // A row of sorted row r is row_token[r] (null: r)
+  const uint32_t* row_off;     // [groups + 1] first sorted row of every group
+  const uint2* tiles;          // (group, first row in group); null: one group of `rows` rows
+  const uint32_t* tile_count;
+  uint32_t rows;
+  const int32_t* slot_table;   // expert -> pool slot, or null
+  PoolDev pool;
+  PoolDev stream;
+  ProjPtrs dense[2];           // routed banks [E, N, K/8], projection 0 and 1
+  ProjPtrs shared[2];          // group == experts: the shared expert
+  int part[2];                 // record part of each projection (0 gate, 1 up, 2 down)
+  const uint16_t* bf16_weight; // router [N, K]
+  const float* bias;           // router, optional [N]
+  void* out;
+  uint32_t* status;
+  uint32_t k_dim, n_dim, experts, a_stride;
+};
+
+struct SortLaunch {
+  const int32_t* inds;         // [tokens, slots]
+  uint32_t* row_off;           // [groups + 1]
+  uint2* tiles;
+  uint32_t* tile_count;
+  uint32_t* row_token;         // [rows]
+  uint32_t* pair_row;          // [tokens * slots]
+  uint32_t* status;
+  uint32_t tokens, slots, experts, shared_rows;
+};
+
+struct CombineLaunch {
+  const uint16_t* rows;        // expert output rows [rows, hidden] bf16
+  const uint32_t* pair_row;    // [tokens * slots]
+  const void* scores;          // [tokens, slots]
+  int score_dtype;
+  const uint32_t* shared_first; // row of token 0's shared expert output in `rows` (with shared_sig)
+  const void* shared_sig;      // [tokens] bf16
+  const void* shared_y;        // or a finished shared term [tokens, hidden] bf16
+  void* out;                   // [tokens, hidden] bf16
+  uint32_t tokens, slots, hidden;
+  int mode;                    // 0 fused combine, 1 generic combine, 2 per-slot rows
+};
+
+uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups);
+hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
+hipError_t launch_sort(const SortLaunch& p, hipStream_t stream);
+hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream);
+hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
+                              uint32_t hidden, hipStream_t stream);
+
 hipError_t launch_front(const FrontLaunch& p, hipStream_t stream);
 hipError_t launch_select(const SelectLaunch& p, hipStream_t stream);
 hipError_t launch_gateup(const GateUpLaunch& p, hipStream_t stream);

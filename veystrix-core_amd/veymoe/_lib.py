@@ -141,7 +141,7 @@ SIGNATURES = {
     "vm_moe_execute": (ctypes.c_int, [ctypes.POINTER(VmMoeArgs), _vp]),
     "vm_router_workspace": (_c_u64, [_c_u32, _c_u32]),
     "vm_router_topk": (ctypes.c_int, [ctypes.POINTER(VmRouterArgs), _vp]),
-    "vm_moe_layer_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
+    "vm_moe_layer_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_layer": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), _vp]),
     "vm_moe_grouped_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_grouped": (ctypes.c_int, [ctypes.POINTER(VmGroupedArgs), _vp]),

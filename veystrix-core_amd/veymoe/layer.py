@@ -140,6 +140,11 @@ class HipSwitchGLU:
             routes = flat_inds
             projections = (self.gate_proj, self.up_proj, self.down_proj)
             slab = None
+        if rows > MAX_DECODE_ROWS and flat.dtype == torch.bfloat16:
+            # the reference's rows > 8 path: per-slot expert outputs (expert_cache.py:1949-2037)
+            from .grouped import grouped_experts
+
+            return grouped_experts(self, flat, flat_inds).reshape(*x.shape[:-1], k, hidden)
         combine = scores is not None and rows <= MAX_DECODE_ROWS
         if combine:
             out = executor._run(flat, routes, *projections, self.inter, False,
@@ -203,8 +208,8 @@ class MoELayer:
         key = (tokens, dtype, x.device)
         ws = self._ws.get(key)
         if ws is None:
-            nbytes = int(lib.vm_moe_layer_workspace(tokens, self.top_k, sw.inter, shared_inter, sw.num_experts,
-                                                    dtype))
+            nbytes = int(lib.vm_moe_layer_workspace(tokens, self.top_k, sw.hidden, sw.inter, shared_inter,
+                                                    sw.num_experts, dtype))
             ws = torch.zeros(nbytes, dtype=torch.uint8, device=x.device)
             self._ws[key] = ws
         a = _lib.VmLayerArgs()
@@ -237,8 +242,10 @@ class MoELayer:
         a.renorm_blend = self.renorm_blend
         return a
 
-    def decode(self, flat: torch.Tensor) -> torch.Tensor:
-        """rows <= 8: the fused decode layer."""
+    def forward(self, flat: torch.Tensor) -> torch.Tensor:
+        """The layer on [rows, hidden]: rows <= 8 run the fused decode kernels,
+        more rows the grouped path (router GEMM, device token-by-expert sort,
+        MFMA grouped experts, generic combine); both inside vm_moe_layer."""
         require_device("x", flat, (torch.bfloat16, torch.float32))
         tokens = flat.shape[0]
         out = torch.empty_like(flat)
@@ -267,16 +274,10 @@ class MoELayer:
         self.last_inds, self.last_scores = inds, scores
         return out
 
+    decode = forward
+    prefill = forward
+
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         hidden = x.shape[-1]
         flat = x.reshape(-1, hidden).contiguous()
-        if flat.shape[0] <= MAX_DECODE_ROWS:
-            return self.decode(flat).reshape(x.shape)
-        return self.prefill(flat).reshape(x.shape)
-
-    # -------------------------------------------------------- prefill ---
-    def prefill(self, flat: torch.Tensor) -> torch.Tensor:
-        """rows > 8: router, grouped experts, generic combine + shared term."""
-        from .grouped import grouped_layer
-
-        return grouped_layer(self, flat)
+        return self.forward(flat).reshape(x.shape)
