@@ -18,6 +18,11 @@ dispatches (hipExtLaunchKernelGGL) in a second, eager pass over the same
 steps; bytes = algorithmic bytes of one launch.  cpu_baseline:
 the C restatement of the same layer (oracle/cmoe.c, OpenMP) on a bounded
 sample of tokens, on this host's cores.
+
+Extra fields (not `value`): "batched" (32 rows per call, Zipf(1.1) routing,
+8 pool-resident layers cycled) and "prefill" (2048 rows per call, 3 layers
+cycled) through the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA
+fraction (algorithmic FLOPs / time / 2.5 PFLOP/s).
 """
 from __future__ import annotations
 
@@ -134,6 +139,84 @@ def cpu_baseline(spec, seed, seconds):
                       f"C restatement oracle/cmoe.c with OpenMP"}
 
 
+BF16_MFMA_PEAK_TFLOPS = 2500.0
+
+
+def grouped_flops(spec, tokens):
+    """Multiply-adds x 2 of one grouped layer call: routed gate/up/down, the
+    shared expert, the router."""
+    expert = 6 * spec.inter * spec.hidden
+    shared = 6 * spec.shared_inter * spec.hidden if spec.shared_inter else 0
+    return tokens * (spec.top_k * expert + shared + 2 * spec.hidden * spec.experts)
+
+
+def grouped_bytes(spec, tokens, distinct):
+    """Algorithmic HBM bytes of one grouped layer call with `distinct` experts routed."""
+    record = spec.layout.record_bytes
+    shared = record if spec.shared_inter else 0
+    seg = spec.hidden // 2 + 2 * (spec.hidden // 32) * 2
+    return distinct * record + shared + seg + spec.experts * spec.hidden * 2 + 2 * tokens * spec.hidden * 2
+
+
+def run_grouped(name, tokens, layers, reps, seed):
+    """One grouped workload: layer calls of `tokens` rows cycling over `layers`
+    pool-resident layers; wall clock over the timed calls, per-kernel HIP
+    event timing in a second pass."""
+    import numpy as np
+    import torch
+
+    from veymoe import _lib, synth
+    from veymoe.device import stream_handle
+
+    device = torch.device("cuda:0")
+    spec = synth.CONFIGS[name]
+    stack, pool = build_stack(spec, layers, device, seed)
+    lib = _lib.lib()
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed + 1)
+    x = torch.randn((layers, tokens, spec.hidden), device=device, generator=gen).to(torch.bfloat16)
+    out = torch.empty_like(x)
+    inds = torch.empty((layers, tokens, spec.top_k), dtype=torch.int32, device=device)
+    scores = torch.empty((layers, tokens, spec.top_k), dtype=torch.bfloat16, device=device)
+    args = [stack[i].layer_args(x[i], out[i], inds[i], scores[i]) for i in range(layers)]
+    refs = [ctypes.byref(a) for a in args]
+    handle = stream_handle()
+    for i in range(layers * 2):
+        _lib.check(lib.vm_moe_layer(refs[i % layers], handle))
+    torch.cuda.synchronize()
+    calls = layers * reps
+    start = time.perf_counter()
+    for i in range(calls):
+        _lib.check(lib.vm_moe_layer(refs[i % layers], handle))
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    lib.vm_timing_reset()
+    lib.vm_timing_enable(1)
+    for i in range(calls):
+        _lib.check(lib.vm_moe_layer(refs[i % layers], handle))
+    torch.cuda.synchronize()
+    lib.vm_timing_enable(0)
+    kernels = {}
+    for fam in ("router", "router_gemm", "select", "sort", "grouped_gateup", "grouped_down", "combine"):
+        total, launches = ctypes.c_double(), ctypes.c_uint64()
+        _lib.check(lib.vm_timing_read(fam.encode(), ctypes.byref(total), ctypes.byref(launches)))
+        if launches.value:
+            kernels[fam] = round(total.value * 1e3 / calls, 2)
+    distinct = float(np.mean([len(np.unique(inds[i].cpu().numpy())) for i in range(layers)]))
+    us = elapsed * 1e6 / calls
+    nbytes = grouped_bytes(spec, tokens, distinct)
+    flops = grouped_flops(spec, tokens)
+    result = {"tokens": tokens, "tok_s": round(tokens / (us * 1e-6), 1), "us_per_layer": round(us, 2),
+              "layers_cycled": layers, "calls": calls, "distinct_experts": round(distinct, 1),
+              "algorithmic_bytes": int(nbytes), "gbps": round(nbytes / (us * 1e3), 1),
+              "tflops": round(flops / (us * 1e6), 2),
+              "mfma_frac": round(flops / (us * 1e6) / BF16_MFMA_PEAK_TFLOPS, 4),
+              "kernels_us": kernels}
+    del stack, pool, args, refs, x, out, inds, scores
+    torch.cuda.empty_cache()
+    return result
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -144,6 +227,11 @@ def main():
     parser.add_argument("--eager", action="store_true", help="launch layer by layer instead of graph replay")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-grouped", action="store_true",
+                        help="skip the batched (32 rows) and prefill (2048 rows) grouped workloads")
+    parser.add_argument("--copy-probe-mib", type=int, default=0,
+                        help="after the timed work, stream this many MiB through one elementwise bf16 kernel "
+                             "(out = in * 1): the reference reading for HBM byte counters")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
@@ -249,6 +337,23 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
+    del graph, stack, pool, call_args, refs
+    torch.cuda.empty_cache()
+    if not args.no_grouped:
+        log("batched decode: 32 rows, Zipf(1.1) routing")
+        result["batched"] = run_grouped("batched", 32, 8, 50, args.seed)
+        log("chunked prefill: 2048 rows")
+        result["prefill"] = run_grouped("prefill", 2048, 3, 8, args.seed)
+    if args.copy_probe_mib:
+        n = args.copy_probe_mib * (1 << 20) // 2
+        probe_in = torch.ones(n, dtype=torch.bfloat16, device=device)
+        probe_out = torch.empty_like(probe_in)
+        torch.cuda.synchronize()
+        torch.mul(probe_in, 1, out=probe_out)
+        torch.cuda.synchronize()
+        result["copy_probe"] = {"mib": args.copy_probe_mib, "kernel": "torch.mul(bf16, 1, out=...)",
+                                "bytes_read": n * 2, "bytes_written": n * 2}
+        del probe_in, probe_out
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(spec, args.seed, args.cpu_seconds)

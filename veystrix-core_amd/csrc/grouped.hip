@@ -60,17 +60,40 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
-// 8 inputs of one packed word -> bf16 pairs (q_n, q_{n+4}) for n < 4, the
-// order pair_activations gives the activations.  (1024 + q) is exact in f16;
-// s * (1024 + q) + (b - 1024 s) is one fp32 fma per value.
-__device__ __forceinline__ void dequant_word(uint32_t word, float s, float b1024, uint32_t out[4]) {
-#pragma unroll
-  for (int n = 0; n < 4; ++n) {
-    const uint32_t m = ((word >> (4 * n)) & 0x000F000Fu) | 0x64006400u;
-    const f16x2_t h = __builtin_bit_cast(f16x2_t, m);
-    out[n] = pack_bf16(fmaf(s, static_cast<float>(h.x), b1024), fmaf(s, static_cast<float>(h.y), b1024));
-  }
+// f16 magic for the nibble decode, kept in a VGPR so that every decode is one
+// v_and_or_b32 (a literal mask and a register magic).
+__device__ __forceinline__ uint32_t f16_magic() {
+  uint32_t m;
+  asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
 }
+
+// 8 inputs of one packed word -> bf16 pairs (q_n, q_{n+4}) for n < 4, the
+// order pair_activations gives the activations.  (1024 + q) and (1024 + 16 q)
+// are exact in f16, so w = s*q + b is one fp32 fma per value:
+// s*(1024 + q) + (b - 1024 s) for the low nibble of a byte and
+// (s/16)*(1024 + 16 q) + (b - 64 s) for the high one.
+struct Dequant {
+  float s, b1024, s16, b64;
+  __device__ __forceinline__ Dequant(uint32_t s_bits, uint32_t b_bits) {
+    s = bf16_to_f32(s_bits);
+    const float b = bf16_to_f32(b_bits);
+    b1024 = fmaf(-1024.0f, s, b);
+    s16 = 0.0625f * s;
+    b64 = fmaf(-64.0f, s, b);
+  }
+  __device__ __forceinline__ void word(uint32_t w, uint32_t magic, uint32_t out[4]) const {
+    const uint32_t w8 = w >> 8;
+    const uint32_t m[4] = {(w & 0x000F000Fu) | magic, (w & 0x00F000F0u) | magic, (w8 & 0x000F000Fu) | magic,
+                           (w8 & 0x00F000F0u) | magic};
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      const f16x2_t h = __builtin_bit_cast(f16x2_t, m[n]);
+      const float sc = n & 1 ? s16 : s, bc = n & 1 ? b64 : b1024;
+      out[n] = pack_bf16(fmaf(sc, static_cast<float>(h.x), bc), fmaf(sc, static_cast<float>(h.y), bc));
+    }
+  }
+};
 
 // bf16 weights: natural pairs (k0 k1)(k2 k3)(k4 k5)(k6 k7) -> (k0 k4)(k1 k5)(k2 k6)(k3 k7)
 __device__ __forceinline__ void permute_word(const uint4 v, uint32_t out[4]) {
@@ -97,27 +120,25 @@ template <>
 struct BChunk<true> {
   uint4 w[kHalves];
   uint32_t s[kHalves], b[kHalves];
-  __device__ __forceinline__ void load(const ProjPtrs& p, bool live, size_t row, uint32_t g0, uint32_t kb,
-                                       uint32_t K) {
-    const uint32_t G = K / kGroup;
+  // p: the projection (uniform), wrow/mrow: byte offsets of this lane's row in
+  // the packed words / the scales and biases; groups past the end are clamped
+  // (their activations are staged as zeros)
+  __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t mrow, uint32_t g0, uint32_t kb,
+                                       uint32_t gmax) {
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
-      const uint32_t g = g0 + 4 * h + kb;
-      const bool l = live && g < G;
-      const size_t wo = row * (K / 8) + g * kWordsPerGroup;
-      const size_t mo = row * G + g;
-      w[h] = ldg16(l ? static_cast<const void*>(p.w + wo) : static_cast<const void*>(g_zero_page));
-      s[h] = ldg_u16(l ? static_cast<const void*>(p.s + mo) : static_cast<const void*>(g_zero_page));
-      b[h] = ldg_u16(l ? static_cast<const void*>(p.b + mo) : static_cast<const void*>(g_zero_page));
+      const uint32_t g = min(g0 + 4 * h + kb, gmax);
+      w[h] = ldg16(reinterpret_cast<const uint8_t*>(p.w) + wrow + g * 16u);
+      s[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.s) + mrow + g * 2u);
+      b[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.b) + mrow + g * 2u);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic) const {
     const int h = st >> 2, i = st & 3;
-    const float sf = bf16_to_f32(s[h]);
-    const float b1024 = fmaf(-1024.0f, sf, bf16_to_f32(b[h]));
+    const Dequant dq(s[h], b[h]);
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
     uint32_t r[4];
-    dequant_word(word, sf, b1024, r);
+    dq.word(word, magic, r);
     return as_operand(r);
   }
 };
@@ -125,18 +146,18 @@ struct BChunk<true> {
 template <>
 struct BChunk<false> {
   uint4 v[kHalves][4];
-  __device__ __forceinline__ void load(const uint16_t* wbf, bool live, size_t row, uint32_t g0, uint32_t kb,
-                                       uint32_t K) {
+  // router: bf16 weights [N, K]; wrow = byte offset of the row
+  __device__ __forceinline__ void load(const uint16_t* wbf, uint32_t wrow, uint32_t, uint32_t g0, uint32_t kb,
+                                       uint32_t gmax) {
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
-      const uint32_t g = g0 + 4 * h + kb;
-      const bool l = live && g < K / kGroup;
-      const uint16_t* src = l ? wbf + row * K + g * kGroup : reinterpret_cast<const uint16_t*>(g_zero_page);
+      const uint32_t g = min(g0 + 4 * h + kb, gmax);
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(wbf) + wrow + g * 64u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 8 * i);
+      for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 16 * i);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t) const {
     uint32_t r[4];
     permute_word(v[st >> 2][st & 3], r);
     return as_operand(r);
@@ -189,11 +210,19 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
 #pragma unroll
       for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
     }
-    if (!ok && tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
+    if (!ok) {  // an unresolved expert: its rows are zero (status flagged)
+      if (tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
+      for (uint32_t i = tid; i < rows * WAVES * NBW * 16; i += WAVES * 64) {
+        const uint32_t r = i / (WAVES * NBW * 16);
+        const uint32_t col = blockIdx.x * WAVES * NBW * 16 + i % (WAVES * NBW * 16);
+        if (col < N) ActBF16::store(p.out, static_cast<size_t>(row0 + r) * N + col, 0.0f);
+      }
+      return;
+    }
   }
 
   // A staging: item it = tid + j * threads -> (row it / kCG, group it % kCG
-  // of the chunk), 64 bytes each
+  // of the chunk), 64 bytes each: eight lanes read one row's 512 bytes
   uint32_t a_off[kItems];
   const uint16_t* a_src[kItems];
   bool a_live_row[kItems];
@@ -234,18 +263,24 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
     }
   };
 
-  // B: lane -> (column lane%16 of each block, group g0 + lane/16)
+  // B: lane -> (column lane%16 of each block, group g0 + lane/16); columns
+  // past N read the last row and are not stored
   const uint32_t bn = lane & 15u, bkb = lane >> 4;
+  uint32_t wrow[NBW], mrow[NBW];
+#pragma unroll
+  for (int nb = 0; nb < NBW; ++nb) {
+    const uint32_t col = min(n_wave + nb * 16 + bn, N - 1);
+    wrow[nb] = Q4 ? col * (K / 2) : col * K * 2;
+    mrow[nb] = col * G * 2;
+  }
   BChunk<Q4> bc[PROJ][NBW], bn_next[PROJ][NBW];
   auto b_load = [&](BChunk<Q4> (&dst)[PROJ][NBW], uint32_t g0) {
 #pragma unroll
     for (int pj = 0; pj < PROJ; ++pj) {
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
-        const uint32_t col = n_wave + nb * 16 + bn;
-        const bool live = ok && col < N;
-        if constexpr (Q4) dst[pj][nb].load(w[pj], live, col, g0, bkb, K);
-        else dst[pj][nb].load(p.bf16_weight, live, col, g0, bkb, K);
+        if constexpr (Q4) dst[pj][nb].load(w[pj], wrow[nb], mrow[nb], g0, bkb, G - 1);
+        else dst[pj][nb].load(p.bf16_weight, wrow[nb], 0u, g0, bkb, G - 1);
       }
     }
   };
@@ -259,6 +294,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
       for (int mb = 0; mb < kMB; ++mb) acc[pj][nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const uint32_t chunks = (G + kCG - 1) / kCG;
+  const uint32_t magic = Q4 ? f16_magic() : 0u;
   a_load(0);
   b_load(bc, 0);
   a_store(0);
@@ -277,7 +313,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
 #pragma unroll
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) bop[pj][nb] = bc[pj][nb].step(st);
+        for (int nb = 0; nb < NBW; ++nb) bop[pj][nb] = bc[pj][nb].step(st, magic);
 #pragma unroll
       for (int mb = 0; mb < kMB; ++mb) {
         if (static_cast<uint32_t>(mb * 16) >= rows) break;  // block-uniform
