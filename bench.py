@@ -22,7 +22,9 @@ sample of tokens, on this host's cores.
 Extra fields (not `value`): "batched" (32 rows per call, Zipf(1.1) routing,
 8 pool-resident layers cycled) and "prefill" (2048 rows per call, 3 layers
 cycled) through the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA
-fraction (algorithmic FLOPs / time / 2.5 PFLOP/s).
+fraction (algorithmic FLOPs / time / 2.5 PFLOP/s); "stack48_lru" (48 layers at
+batch 1 with a 3,051-slot LRU pool, Zipf routing, misses staged from pinned
+host memory): tokens/s through the stack, hit rate, staged bytes.
 """
 from __future__ import annotations
 
@@ -217,6 +219,92 @@ def run_grouped(name, tokens, layers, reps, seed):
     return result
 
 
+def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_000_000_000, bias_scale=1.0):
+    """The 48-layer stack at batch 1 with an LRU expert pool of `pool_bytes`
+    (3,051 slots at 6 GB, the reference's sizing) and Zipf(1.1) routing; misses
+    are staged from pinned host records with hipMemcpyAsync on a side stream.
+    The host store holds `store_records` distinct records aliased over the
+    24,576 (layer, expert) ids (the bytes moved per miss are the same).
+    `bias_scale` multiplies the log-Zipf logit bias (1 = the stated recipe)."""
+    import torch
+
+    from veymoe import assemble, synth
+    from veymoe.executor import Q4G32Projection
+    from veymoe.layer import HipSwitchGLU, MoELayer, QuantizedMLP, RouterLinear
+    from veymoe.pool import ExpertPool, HostRecordStore
+
+    device = torch.device("cuda:0")
+    spec = synth.CONFIGS["stack"]
+    layout = spec.layout
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    pool = ExpertPool.from_bytes(layout, pool_bytes, layers=spec.layers, experts=spec.experts, device=device)
+    store = HostRecordStore(layout, store_records)
+    staging = torch.empty((256, layout.record_stride), dtype=torch.uint8, device=device)
+    for start in range(0, store_records, 256):
+        n = min(256, store_records - start)
+        assemble.random_records_(staging[:n], layout, gen)
+        store.buffer[start:start + n].copy_(staging[:n])
+    del staging
+    for layer in range(spec.layers):
+        for expert in range(spec.experts):
+            store.alias(layer, expert, (layer * spec.experts + expert) % store_records)
+
+    def q4(out_w, in_w):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (1, out_w, in_w // 8), dtype=torch.int32, device=device,
+                          generator=gen)
+        s = torch.empty((1, out_w, in_w // 32), device=device).uniform_(0.005, 0.02, generator=gen)
+        b = torch.empty((1, out_w, in_w // 32), device=device).uniform_(-0.1, 0.1, generator=gen)
+        return Q4G32Projection(w, s.to(torch.bfloat16), b.to(torch.bfloat16))
+
+    layers = []
+    for layer in range(spec.layers):
+        router = (torch.randn((spec.experts, spec.hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
+        bias = torch.from_numpy(synth.router_bias(spec, seed, layer) * bias_scale).to(device)
+        switch = HipSwitchGLU(spec.hidden, spec.inter, spec.experts, pool=pool, layer_id=layer, host_store=store)
+        shared = QuantizedMLP(q4(spec.shared_inter, spec.hidden), q4(spec.shared_inter, spec.hidden),
+                              q4(spec.hidden, spec.shared_inter))
+        layers.append(MoELayer(RouterLinear(router, bias), switch, spec.top_k, shared_expert=shared,
+                               shared_expert_gate=q4(1, spec.hidden)))
+    x = torch.randn((warm_tokens + tokens, spec.layers, spec.hidden), device=device, generator=gen)
+    x = x.to(torch.bfloat16)
+    for t in range(warm_tokens):
+        for layer in range(spec.layers):
+            layers[layer](x[t, layer:layer + 1])
+    torch.cuda.synchronize()
+    hits0 = sum(m.switch_mlp.hits for m in layers)
+    misses0 = sum(m.switch_mlp.misses for m in layers)
+    staged0 = pool.bytes_staged
+    start = time.perf_counter()
+    for t in range(warm_tokens, warm_tokens + tokens):
+        for layer in range(spec.layers):
+            layers[layer](x[t, layer:layer + 1])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - start
+    hits = sum(m.switch_mlp.hits for m in layers) - hits0
+    misses = sum(m.switch_mlp.misses for m in layers) - misses0
+    staged = pool.bytes_staged - staged0
+    # pinned host -> HBM copy rate of one large transfer, the bound of the miss path
+    big = store.buffer[: min(store_records, 512)]
+    dst = torch.empty(big.shape, dtype=torch.uint8, device=device)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    dst.copy_(big, non_blocking=True)
+    torch.cuda.synchronize()
+    h2d = big.numel() / (time.perf_counter() - t0) / 1e9
+    result = {"tokens": tokens, "layers": spec.layers, "bias_scale": bias_scale,
+              "tok_s": round(tokens / elapsed, 2),
+              "ms_per_token": round(elapsed * 1e3 / tokens, 3), "pool_slots": pool.slots,
+              "hit_rate": round(hits / max(1, hits + misses), 4), "misses_per_token": round(misses / tokens, 1),
+              "staged_gb_per_token": round(staged / tokens / 1e9, 3),
+              "staged_gbps": round(staged / elapsed / 1e9, 2), "pinned_h2d_gbps": round(h2d, 2),
+              "host_store": f"{store_records} distinct pinned records ({store_records * layout.record_stride / 1e9:.1f} GB) "
+                            f"aliased over {spec.layers * spec.experts} (layer, expert) ids"}
+    del layers, pool, store, x, big, dst
+    torch.cuda.empty_cache()
+    return result
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -229,6 +317,8 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-grouped", action="store_true",
                         help="skip the batched (32 rows) and prefill (2048 rows) grouped workloads")
+    parser.add_argument("--no-stack", action="store_true",
+                        help="skip the 48-layer stack with the LRU pool and host-staged misses")
     parser.add_argument("--copy-probe-mib", type=int, default=0,
                         help="after the timed work, stream this many MiB through one elementwise bf16 kernel "
                              "(out = in * 1): the reference reading for HBM byte counters")
@@ -344,6 +434,11 @@ def main():
         result["batched"] = run_grouped("batched", 32, 8, 50, args.seed)
         log("chunked prefill: 2048 rows")
         result["prefill"] = run_grouped("prefill", 2048, 3, 8, args.seed)
+    if not args.no_stack:
+        log("48-layer stack, LRU pool of 6 GB, misses from pinned host")
+        # the stated Zipf(1.1) recipe, and its logit bias scaled to reach the ~60% hit rate
+        result["stack48_lru"] = {"zipf_recipe": run_stack(args.seed),
+                                 "hit_rate_60": run_stack(args.seed, bias_scale=0.45)}
     if args.copy_probe_mib:
         n = args.copy_probe_mib * (1 << 20) // 2
         probe_in = torch.ones(n, dtype=torch.bfloat16, device=device)

@@ -191,6 +191,7 @@ class MoELayer:
         self.last_inds = None
         self.last_scores = None
         self._ws = {}
+        self._args_cache = {}
 
     @property
     def hidden(self) -> int:
@@ -249,9 +250,19 @@ class MoELayer:
         require_device("x", flat, (torch.bfloat16, torch.float32))
         tokens = flat.shape[0]
         out = torch.empty_like(flat)
-        inds = torch.empty((tokens, self.top_k), dtype=torch.int32, device=flat.device)
-        scores = torch.empty((tokens, self.top_k), dtype=flat.dtype, device=flat.device)
-        args = self.layer_args(flat, out, inds, scores)
+        # the C arguments are built once per (rows, dtype, device); a call only
+        # patches the activation pointers (inds/scores live in per-layer buffers)
+        key = (tokens, flat.dtype, flat.device)
+        cached = self._args_cache.get(key)
+        if cached is None:
+            inds = torch.empty((tokens, self.top_k), dtype=torch.int32, device=flat.device)
+            scores = torch.empty((tokens, self.top_k), dtype=flat.dtype, device=flat.device)
+            cached = (self.layer_args(flat, out, inds, scores), inds, scores)
+            self._args_cache[key] = cached
+        args, inds, scores = cached
+        args.x = ptr(flat)
+        args.output = ptr(out)
+        args.phases = 0
         lib = _lib.lib()
         sw = self.switch_mlp
         if sw.pool is not None and not sw._pool_fully_resident():

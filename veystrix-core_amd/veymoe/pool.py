@@ -89,6 +89,8 @@ class ExpertPool:
         self.misses = 0
         self.bytes_staged = 0
         self._copy_stream = None
+        self._pinned_table = None
+        self._table_event = None
 
     @classmethod
     def from_bytes(cls, layout: RecordLayout, size_bytes: int, **kwargs):
@@ -171,11 +173,22 @@ class ExpertPool:
         return self.slot_table[layer]
 
     def sync_tables(self) -> None:
-        """Upload the slot-table rows changed since the last call (ordered on the
-        current stream before any kernel launched after it)."""
+        """Upload the slot-table rows changed since the last call, asynchronously
+        on the current stream (ordered before any kernel launched after it),
+        from a pinned mirror that is not rewritten before the last upload ran."""
+        if not self._dirty:
+            return
+        if self._pinned_table is None:
+            self._pinned_table = torch.empty((self.layers, self.experts), dtype=torch.int32,
+                                             pin_memory=self.device.type == "cuda")
+        if self._table_event is not None:
+            self._table_event.synchronize()
+        stream = torch.cuda.current_stream(self.device)
         for layer in sorted(self._dirty):
-            row = torch.from_numpy(self._host_table[layer].copy())
-            self.slot_table[layer].copy_(row, non_blocking=False)
+            self._pinned_table[layer].numpy()[:] = self._host_table[layer]
+            self.slot_table[layer].copy_(self._pinned_table[layer], non_blocking=True)
+        self._table_event = torch.cuda.Event()
+        self._table_event.record(stream)
         self._dirty.clear()
 
     def place(self, layer: int, expert: int, slot: int) -> None:
