@@ -142,6 +142,21 @@ def cpu_baseline(spec, seed, seconds):
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0
+TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_decode_grouped_pmc.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the decode gate/up kernel from the committed
+    rocprofv3 FETCH_SIZE/WRITE_SIZE summary (counters scaled by a copy kernel
+    of known size), or None when the summary is absent."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 def grouped_flops(spec, tokens):
@@ -402,7 +417,7 @@ def main():
     gateup = kernels["gateup"]
     roofline = {"bound": "hbm", "kernel": "gateup (routed + shared gate/up Q4 GEMV + SwiGLU)",
                 "achieved": gateup["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(gateup["gbps"] / HBM_PEAK_GBPS, 4), "traffic": None}
+                "frac": round(gateup["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic()}
     result = {
         "metric": "MoE-layer decode tok/s + achieved HBM GB/s (% peak); prefill tok/s at 2048",
         "value": round(steps / elapsed, 1),

@@ -19,7 +19,8 @@
  *                      flashnext_native_moe_execute     models/flashnext/tests/bench/metal_runtime_native.mm:258-395
  *   vm_router_topk     router softmax/top-k/renorm      models/flashnext/adaptive_topk.py:59-65,257-262
  *                                                       models/flashnext/compiled.py:61-71
- *   vm_moe_layer       _moe_call decode branch          models/flashnext/adaptive_topk.py:54-293 (rows <= 8)
+ *   vm_moe_layer       _moe_call                        models/flashnext/adaptive_topk.py:54-293
+ *                      (rows <= 8: custom-kernel branch :289-293; rows > 8: generic branch :275-278)
  *   vm_moe_grouped     _one_pass/_issue gather_qmm path models/flashnext/expert_cache.py:1949-2037 (rows > 8)
  *   vm_weighted_combine weighted_combine                models/flashnext/metal_runtime.py:145-191
  *   vm_pool_stage      ExpertPool.fill/_fill_part       models/flashnext/expert_pool.py:201-220,258-287
