@@ -39,6 +39,15 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWaves = kBlock / 64;
+// block shapes of the full-width (hidden >= 2048) decode GEMVs: output rows per
+// lane group in gate/up, row groups per block in down
+#ifndef VM_GATEUP_ROWS
+#define VM_GATEUP_ROWS 2
+#endif
+#ifndef VM_DOWN_QUADS
+#define VM_DOWN_QUADS 2
+#endif
+constexpr int kGateupRowsPerLane = VM_GATEUP_ROWS;
 constexpr int kMaxExpertsPerLane = 8;  // expert_count <= 512
 
 template <class A>
@@ -661,7 +670,7 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
 
 constexpr int kDownMaxSlots = 12;                         // MAX_TOP_K (10) + shared, rounded up
 constexpr int kDownSlotsPerWave = kDownMaxSlots / kWaves;  // wave w owns slots w, w+4, w+8
-constexpr int kDownQuads = 2;                             // row groups of 64/LPR rows per block
+constexpr int kDownQuads = VM_DOWN_QUADS;                 // row groups of 64/LPR rows per block
 
 // LPR = I/32 lanes per row (one group each); a block covers RB rows of all
 // slots of one token.
@@ -872,7 +881,7 @@ hipError_t gateup_dispatch(const GateUpLaunch& p, hipStream_t stream) {
     case 32: return gateup_go<A, 32, 1, 2>(p, stream);
     default: break;
   }
-  if (gi <= 1) return gateup_go<A, 64, 1, 4>(p, stream);
+  if (gi <= 1) return gateup_go<A, 64, 1, kGateupRowsPerLane>(p, stream);
   if (gi <= 2) return gateup_go<A, 64, 2, 2>(p, stream);
   return gateup_go<A, 64, 4, 1>(p, stream);
 }
