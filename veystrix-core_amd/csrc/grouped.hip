@@ -8,13 +8,18 @@
 //            the expert changes no result, since every output row is its own
 //            set of dot products.  The shared expert is one more group whose
 //            rows are all the tokens.
-//   gemm     one workgroup per (tile of <= 64 rows of one group, tile of output
-//            features).  K runs in chunks of eight 32-input groups: the A rows
-//            are staged in LDS (double buffered, pair-permuted to match the
-//            dequantised weights), each lane dequantises one 16-byte Q4 group
-//            per chunk and projection into bf16 (f16 magic number + v_fma_mix
-//            + v_cvt_pk_bf16_f32) and feeds v_mfma_f32_16x16x32_bf16 with fp32
-//            accumulation.  Epilogues: SwiGLU of gate and up, bf16 rows (down),
+//   gemm     one workgroup per (tile of <= 64 rows of one group, slice of output
+//            features).  Workgroups are dealt to the eight XCDs round-robin;
+//            the slices of one row tile take blocks of the same XCD so that
+//            they share its L2 copy of the tile's A rows.  K runs in chunks of
+//            eight 32-input groups: the A rows are staged in LDS (double
+//            buffered, 32 lanes per 512-byte row segment, pair-permuted to
+//            match the dequantised weights), each lane dequantises one
+//            16-byte Q4 group per chunk and projection into bf16 (f16 magic
+//            number + v_fma_mix + v_cvt_pk_bf16_f32) and feeds
+//            v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The MFMA loop
+//            is specialised on the number of 16-row blocks in use, so it has
+//            no branch.  Epilogues: SwiGLU of gate and up, bf16 rows (down),
 //            router logits (bf16 weights).
 //   combine  per token, the expert rows in slot order with the router scores
 //            and the shared term.
@@ -37,7 +42,10 @@ namespace {
 constexpr int kGB = 256;                 // threads per block of the small kernels
 constexpr int kBM = kGroupedRows;        // rows per tile
 constexpr int kMB = kBM / 16;            // MFMA row blocks
-constexpr int kCG = 8;                   // 32-input groups per K chunk (a 128-byte line per weight row)
+#ifndef VM_GCG
+#define VM_GCG 8
+#endif
+constexpr int kCG = VM_GCG;              // 32-input groups per K chunk (8: a 128-byte line per weight row)
 constexpr int kHalves = kCG / 4;         // groups per lane and chunk
 constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
 constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
@@ -121,13 +129,27 @@ struct BChunk<true> {
   uint4 w[kHalves];
   uint32_t s[kHalves], b[kHalves];
   // p: the projection (uniform), wrow/mrow: byte offsets of this lane's row in
-  // the packed words / the scales and biases; groups past the end are clamped
-  // (their activations are staged as zeros)
+  // the packed words / the scales and biases.  A chunk inside the row takes
+  // uniform chunk offsets (no per-lane address arithmetic); in the tail chunk
+  // groups past the end are clamped (their activations are staged as zeros).
   __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t mrow, uint32_t g0, uint32_t kb,
-                                       uint32_t gmax) {
+                                       uint32_t G, bool tail) {
+    if (!tail) {
+      const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.w) + g0 * 16u;
+      const uint8_t* sb = reinterpret_cast<const uint8_t*>(p.s) + g0 * 2u;
+      const uint8_t* bb = reinterpret_cast<const uint8_t*>(p.b) + g0 * 2u;
+      const uint32_t wl = wrow + kb * 16u, ml = mrow + kb * 2u;
+#pragma unroll
+      for (int h = 0; h < kHalves; ++h) {
+        w[h] = ldg16(wb + wl + h * 64u);
+        s[h] = ldg_u16(sb + ml + h * 8u);
+        b[h] = ldg_u16(bb + ml + h * 8u);
+      }
+      return;
+    }
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
-      const uint32_t g = min(g0 + 4 * h + kb, gmax);
+      const uint32_t g = min(g0 + 4 * h + kb, G - 1);
       w[h] = ldg16(reinterpret_cast<const uint8_t*>(p.w) + wrow + g * 16u);
       s[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.s) + mrow + g * 2u);
       b[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.b) + mrow + g * 2u);
@@ -148,10 +170,10 @@ struct BChunk<false> {
   uint4 v[kHalves][4];
   // router: bf16 weights [N, K]; wrow = byte offset of the row
   __device__ __forceinline__ void load(const uint16_t* wbf, uint32_t wrow, uint32_t, uint32_t g0, uint32_t kb,
-                                       uint32_t gmax) {
+                                       uint32_t G, bool tail) {
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
-      const uint32_t g = min(g0 + 4 * h + kb, gmax);
+      const uint32_t g = tail ? min(g0 + 4 * h + kb, G - 1) : g0 + 4 * h + kb;
       const uint8_t* src = reinterpret_cast<const uint8_t*>(wbf) + wrow + g * 64u;
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 16 * i);
@@ -164,102 +186,61 @@ struct BChunk<false> {
   }
 };
 
-// EPI: 0 SwiGLU of projections 0 (gate) and 1 (up) -> bf16 [rows, N];
-//      1 bf16 rows -> [rows, N]; 2 router logits (bf16 weights) -> fp32 [rows, N].
-template <int EPI, int WAVES, int NBW, int PROJ>
-__global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
-  static_assert(WAVES >= 4, "the A staging uses the first 256 threads");
+// The tile body for MBU 16-row blocks in use (rows <= 16 * MBU): the A
+// staging covers those rows only and the MFMA loops carry no branch, so the
+// LDS reads of a step and the MFMAs of neighbouring steps can be scheduled
+// freely.
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU>
+__device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjPtrs (&w)[PROJ], uint32_t row0,
+                                             uint32_t rows, uint32_t slice, uint8_t* s_a0) {
   constexpr bool Q4 = EPI != kEpiLogits;
   constexpr int kThreads = WAVES * 64;
-  constexpr int kItems = kBM * kCG / kThreads;  // A staging items per thread
-  extern __shared__ uint4 s_dyn[];               // two A stages of kStageBytes
-  uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
+  constexpr int kUnits = kCG * 4;                                // 16-byte A units per row and chunk
+  constexpr int kItemsAll = MBU * 16 * kUnits;                  // A units per stage
+  constexpr int kItems = (kItemsAll + kThreads - 1) / kThreads;  // per thread
+  constexpr bool kAllItems = kItemsAll % kThreads == 0;
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
-
-  // the tile: rows [row0, row0 + rows) of `group`
-  uint32_t group = 0, row0, rows;
-  if (p.tiles != nullptr) {
-    if (blockIdx.y >= *p.tile_count) return;
-    const uint2 td = p.tiles[blockIdx.y];
-    group = td.x;
-    row0 = p.row_off[group] + td.y;
-    rows = min(p.row_off[group + 1] - row0, static_cast<uint32_t>(kBM));
-  } else {
-    row0 = blockIdx.y * kBM;
-    if (row0 >= p.rows) return;
-    rows = min(p.rows - row0, static_cast<uint32_t>(kBM));
-  }
   const uint32_t K = p.k_dim, N = p.n_dim, G = K / kGroup;
-  const uint32_t n_wave = (blockIdx.x * WAVES + wave) * NBW * 16;
+  const uint32_t n_wave = (slice * WAVES + wave) * NBW * 16;
 
-  // the group's weights
-  ProjPtrs w[PROJ];
-  bool ok = true;
-  if constexpr (Q4) {
-    if (group >= p.experts) {
-#pragma unroll
-      for (int pj = 0; pj < PROJ; ++pj) w[pj] = p.shared[pj];
-      ok = w[0].w != nullptr;
-    } else {
-      uint32_t index = 0;
-      const int kind = resolve_word(group, p.slot_table, p.experts, p.pool, &p.stream, p.dense[0].w != nullptr, index);
-      ok = kind != kSrcNone;
-#pragma unroll
-      for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
-    }
-    if (!ok) {  // an unresolved expert: its rows are zero (status flagged)
-      if (tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
-      for (uint32_t i = tid; i < rows * WAVES * NBW * 16; i += WAVES * 64) {
-        const uint32_t r = i / (WAVES * NBW * 16);
-        const uint32_t col = blockIdx.x * WAVES * NBW * 16 + i % (WAVES * NBW * 16);
-        if (col < N) ActBF16::store(p.out, static_cast<size_t>(row0 + r) * N + col, 0.0f);
-      }
-      return;
-    }
-  }
-
-  // A staging: item it = tid + j * threads -> (row it / kCG, group it % kCG
-  // of the chunk), 64 bytes each: eight lanes read one row's 512 bytes
-  uint32_t a_off[kItems];
+  // A staging: unit it = tid + j * threads -> (row it / kUnits, 16-byte unit
+  // it % kUnits of the chunk): 32 consecutive lanes read one row's 512
+  // contiguous bytes, so a wave's load covers whole cache lines.  Rows past
+  // the tile repeat its first row: an MFMA output row depends on its own A
+  // row only, and those rows are not stored.
+  uint32_t a_off[kItems], a_u[kItems];
   const uint16_t* a_src[kItems];
-  bool a_live_row[kItems];
-  uint32_t a_q[kItems];
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const uint32_t it = tid + j * kThreads;
-    const uint32_t r = it / kCG, q = it % kCG;
-    a_live_row[j] = r < rows;
-    const uint32_t arow = a_live_row[j] ? (p.row_token != nullptr ? p.row_token[row0 + r] : row0 + r) : 0u;
-    a_src[j] = p.a + static_cast<size_t>(arow) * p.a_stride;
-    a_q[j] = q;
-    a_off[j] = r * kRowBytes + q * 64;
+    const uint32_t r = it / kUnits, u = it % kUnits;
+    const uint32_t rr = r < rows ? r : 0u;
+    const uint32_t arow = p.row_token != nullptr ? p.row_token[row0 + rr] : row0 + rr;
+    a_src[j] = p.a + static_cast<size_t>(arow) * p.a_stride + u * 8;
+    a_u[j] = u;
+    a_off[j] = r * kRowBytes + u * 16;
   }
-  uint4 ar[kItems][4];
-  auto a_load = [&](uint32_t g0) {
+  uint4 ar[kItems];
+  auto a_load = [&](uint32_t g0, bool tail) {
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
-      const uint32_t g = g0 + a_q[j];
-      const bool live = a_live_row[j] && g < G;
-      const uint16_t* src = live ? a_src[j] + g * kGroup : reinterpret_cast<const uint16_t*>(g_zero_page);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ar[j][i] = ldg16(src + 8 * i);
+      if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
+      const uint16_t* src = a_src[j] + g0 * kGroup;
+      if (tail && g0 + a_u[j] / 4 >= G) src = reinterpret_cast<const uint16_t*>(g_zero_page);
+      ar[j] = ldg16(src);
     }
   };
   auto a_store = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
-      uint32_t raw[16], xp[16];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        raw[4 * i] = ar[j][i].x; raw[4 * i + 1] = ar[j][i].y; raw[4 * i + 2] = ar[j][i].z; raw[4 * i + 3] = ar[j][i].w;
-      }
-      pair_activations(raw, xp);
-      uint4* dst = reinterpret_cast<uint4*>(s_a0 + buf * kStageBytes + a_off[j]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = make_uint4(xp[4 * i], xp[4 * i + 1], xp[4 * i + 2], xp[4 * i + 3]);
+      if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
+      const uint32_t a = ar[j].x, b = ar[j].y, c = ar[j].z, d = ar[j].w;
+      *reinterpret_cast<uint4*>(s_a0 + buf * kStageBytes + a_off[j]) =
+          make_uint4((a & 0xffffu) | (c << 16), (a >> 16) | (c & 0xffff0000u),  // (x0, x4) (x1, x5)
+                     (b & 0xffffu) | (d << 16), (b >> 16) | (d & 0xffff0000u));  // (x2, x6) (x3, x7)
     }
   };
 
@@ -273,66 +254,73 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
     wrow[nb] = Q4 ? col * (K / 2) : col * K * 2;
     mrow[nb] = col * G * 2;
   }
-  BChunk<Q4> bc[PROJ][NBW], bn_next[PROJ][NBW];
-  auto b_load = [&](BChunk<Q4> (&dst)[PROJ][NBW], uint32_t g0) {
+  BChunk<Q4> b0[PROJ][NBW], b1[PROJ][NBW];
+  auto b_load = [&](BChunk<Q4> (&dst)[PROJ][NBW], uint32_t g0, bool tail) {
 #pragma unroll
     for (int pj = 0; pj < PROJ; ++pj) {
 #pragma unroll
       for (int nb = 0; nb < NBW; ++nb) {
-        if constexpr (Q4) dst[pj][nb].load(w[pj], wrow[nb], mrow[nb], g0, bkb, G - 1);
-        else dst[pj][nb].load(p.bf16_weight, wrow[nb], 0u, g0, bkb, G - 1);
+        if constexpr (Q4) dst[pj][nb].load(w[pj], wrow[nb], mrow[nb], g0, bkb, G, tail);
+        else dst[pj][nb].load(p.bf16_weight, wrow[nb], 0u, g0, bkb, G, tail);
       }
     }
   };
 
-  f32x4_t acc[PROJ][NBW][kMB];
+  f32x4_t acc[PROJ][NBW][MBU];
 #pragma unroll
   for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
     for (int nb = 0; nb < NBW; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) acc[pj][nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int mb = 0; mb < MBU; ++mb) acc[pj][nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   const uint32_t chunks = (G + kCG - 1) / kCG;
   const uint32_t magic = Q4 ? f16_magic() : 0u;
-  a_load(0);
-  b_load(bc, 0);
+  const uint32_t am = lane & 15u, akb = lane >> 4;
+  const uint32_t a_lane = am * kRowBytes + akb * 64;
+  auto compute = [&](int buf, const BChunk<Q4> (&bc)[PROJ][NBW]) {
+    const uint8_t* s_a = s_a0 + buf * kStageBytes + a_lane;
+#pragma unroll
+    for (int st = 0; st < kSteps; ++st) {
+      bf16x8_t aop[MBU];
+#pragma unroll
+      for (int mb = 0; mb < MBU; ++mb)
+        aop[mb] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
+                                                   s_a + mb * 16 * kRowBytes + (st >> 2) * 256 + (st & 3) * 16));
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) {
+          const bf16x8_t bop = bc[pj][nb].step(st, magic);
+#pragma unroll
+          for (int mb = 0; mb < MBU; ++mb)
+            acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
+        }
+    }
+  };
+  // only a K that is not a multiple of the chunk has a tail chunk
+  auto tail_chunk = [&](uint32_t c) { return TAIL && (c + 1) * kCG > G; };
+  // Loads run one chunk ahead.  The copy of the next chunk's B registers
+  // makes the end of a chunk wait for them; an unrolled ping-pong without
+  // that wait, and a third register set, both measured slower here.
+  a_load(0, tail_chunk(0));
+  b_load(b0, 0, tail_chunk(0));
   a_store(0);
   __syncthreads();
-  const uint32_t am = lane & 15u, akb = lane >> 4;
   for (uint32_t c = 0; c < chunks; ++c) {
     const int buf = c & 1;
     const bool more = c + 1 < chunks;
     if (more) {
-      a_load((c + 1) * kCG);
-      b_load(bn_next, (c + 1) * kCG);
+      a_load((c + 1) * kCG, tail_chunk(c + 1));
+      b_load(b1, (c + 1) * kCG, tail_chunk(c + 1));
     }
-#pragma unroll
-    for (int st = 0; st < kSteps; ++st) {
-      bf16x8_t bop[PROJ][NBW];
-#pragma unroll
-      for (int pj = 0; pj < PROJ; ++pj)
-#pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) bop[pj][nb] = bc[pj][nb].step(st, magic);
-#pragma unroll
-      for (int mb = 0; mb < kMB; ++mb) {
-        if (static_cast<uint32_t>(mb * 16) >= rows) break;  // block-uniform
-        const uint4 av = *reinterpret_cast<const uint4*>(
-            s_a0 + buf * kStageBytes + (mb * 16 + am) * kRowBytes + ((st >> 2) * 4 + akb) * 64 + (st & 3) * 16);
-        const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, av);
-#pragma unroll
-        for (int pj = 0; pj < PROJ; ++pj)
-#pragma unroll
-          for (int nb = 0; nb < NBW; ++nb)
-            acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, bop[pj][nb], acc[pj][nb][mb], 0, 0, 0);
-      }
-    }
+    compute(buf, b0);
     if (more) {
       a_store(buf ^ 1);
 #pragma unroll
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) bc[pj][nb] = bn_next[pj][nb];
+        for (int nb = 0; nb < NBW; ++nb) b0[pj][nb] = b1[pj][nb];
     }
     __syncthreads();
   }
@@ -343,7 +331,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
     const uint32_t col = n_wave + nb * 16 + bn;
     if (col >= N) continue;
 #pragma unroll
-    for (int mb = 0; mb < kMB; ++mb) {
+    for (int mb = 0; mb < MBU; ++mb) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t r = mb * 16 + 4 * bkb + i;
@@ -352,7 +340,7 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
         if constexpr (EPI == kEpiSwiglu) {
           const float gv = round_bf16(acc[0][nb][mb][i]);
           const float uv = round_bf16(acc[PROJ - 1][nb][mb][i]);
-          ActBF16::store(p.out, o, ok ? swiglu_act<ActBF16>(gv, uv) : 0.0f);
+          ActBF16::store(p.out, o, swiglu_act<ActBF16>(gv, uv));
         } else if constexpr (EPI == kEpiRows) {
           ActBF16::store(p.out, o, round_bf16(acc[0][nb][mb][i]));
         } else {
@@ -363,6 +351,84 @@ __global__ __launch_bounds__(WAVES * 64) void k_grouped(GroupedLaunch p) {
       }
     }
   }
+}
+
+// EPI: 0 SwiGLU of projections 0 (gate) and 1 (up) -> bf16 [rows, N];
+//      1 bf16 rows -> [rows, N]; 2 router logits (bf16 weights) -> fp32 [rows, N].
+// TAIL: K is not a multiple of the chunk (kCG groups); the last chunk clamps.
+#ifndef VM_G_WAVES_PER_EU
+#define VM_G_WAVES_PER_EU 1
+#endif
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(VM_G_WAVES_PER_EU)))
+void k_grouped(GroupedLaunch p) {
+  static_assert(kBM % 16 == 0 && kBM <= 64, "tiles are one to four 16-row blocks");
+  constexpr bool Q4 = EPI != kEpiLogits;
+  extern __shared__ uint4 s_dyn[];  // two A stages of kStageBytes
+  uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
+  const uint32_t tid = threadIdx.x;
+
+  // XCD-aware order: workgroups are dealt to the eight XCDs round-robin, so
+  // block L runs on XCD L % 8.  The column slices of one row tile take
+  // consecutive blocks of the same XCD and share its L2 copy of the tile's A
+  // rows; eight row tiles run side by side, one per XCD.  The grid is
+  // slices * (tile bound rounded up to a multiple of 8).
+  const uint32_t slices = (p.n_dim + WAVES * NBW * 16 - 1) / (WAVES * NBW * 16);
+  const uint32_t lin = blockIdx.x, r8 = lin >> 3;
+  const uint32_t slice = r8 % slices;
+  const uint32_t tile = (r8 / slices) * 8 + (lin & 7u);
+
+  // the tile: rows [row0, row0 + rows) of `group`
+  uint32_t group = 0, row0, rows;
+  if (p.tiles != nullptr) {
+    if (tile >= *p.tile_count) return;
+    const uint2 td = p.tiles[tile];
+    group = td.x;
+    row0 = p.row_off[group] + td.y;
+    rows = min(p.row_off[group + 1] - row0, static_cast<uint32_t>(kBM));
+  } else {
+    row0 = tile * kBM;
+    if (row0 >= p.rows) return;
+    rows = min(p.rows - row0, static_cast<uint32_t>(kBM));
+  }
+  const uint32_t K = p.k_dim, N = p.n_dim;
+
+  // the group's weights
+  ProjPtrs w[PROJ];
+  if constexpr (Q4) {
+    bool ok = true;
+    if (group >= p.experts) {
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) w[pj] = p.shared[pj];
+      ok = w[0].w != nullptr;
+    } else {
+      uint32_t index = 0;
+      const int kind = resolve_word(group, p.slot_table, p.experts, p.pool, &p.stream, p.dense[0].w != nullptr, index);
+      ok = kind != kSrcNone;
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
+    }
+    if (!ok) {  // an unresolved expert: its rows are zero (status flagged)
+      if (tid == 0 && slice == 0) flag(p.status, 1u);
+      for (uint32_t i = tid; i < rows * WAVES * NBW * 16; i += WAVES * 64) {
+        const uint32_t r = i / (WAVES * NBW * 16);
+        const uint32_t col = slice * WAVES * NBW * 16 + i % (WAVES * NBW * 16);
+        if (col < N) ActBF16::store(p.out, static_cast<size_t>(row0 + r) * N + col, 0.0f);
+      }
+      return;
+    }
+  }
+  const uint32_t mbu = (rows + 15) / 16;  // block-uniform, 1..kMB
+  if constexpr (kMB >= 4) {
+    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4>(p, w, row0, rows, slice, s_a0);
+  }
+  if constexpr (kMB >= 3) {
+    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3>(p, w, row0, rows, slice, s_a0);
+  }
+  if constexpr (kMB >= 2) {
+    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2>(p, w, row0, rows, slice, s_a0);
+  }
+  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1>(p, w, row0, rows, slice, s_a0);
 }
 
 // ------------------------------------------------------------------ sort ---
@@ -530,34 +596,56 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
   return hipGetLastError();
 }
 
-template <int EPI, int WAVES, int NBW, int PROJ>
-hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
   constexpr uint32_t lds = 2 * kStageBytes;
+  auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL>;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_grouped<EPI, WAVES, NBW, PROJ>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
     attr = true;
   }
   const uint32_t cols = WAVES * NBW * 16;
-  const dim3 grid((p.n_dim + cols - 1) / cols, max_tiles);
+  const dim3 grid(((p.n_dim + cols - 1) / cols) * ((max_tiles + 7) / 8 * 8));
   hipEvent_t start = nullptr, stop = nullptr;
   if (timing_events(family, &start, &stop))
-    hipExtLaunchKernelGGL((k_grouped<EPI, WAVES, NBW, PROJ>), grid, dim3(WAVES * 64), lds, stream, start, stop, 0, p);
+    hipExtLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, start, stop, 0, p);
   else
-    hipLaunchKernelGGL((k_grouped<EPI, WAVES, NBW, PROJ>), grid, dim3(WAVES * 64), lds, stream, p);
+    hipLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, p);
   return hipGetLastError();
+}
+
+template <int EPI, int WAVES, int NBW, int PROJ>
+hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  if ((p.k_dim / kGroup) % kCG != 0) return grouped_go_k<EPI, WAVES, NBW, PROJ, true>(family, p, max_tiles, stream);
+  return grouped_go_k<EPI, WAVES, NBW, PROJ, false>(family, p, max_tiles, stream);
 }
 
 }  // namespace
 
 uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups) { return (rows + kBM - 1) / kBM + groups; }
 
+// block shapes (waves, 16-column blocks per wave) of the gate/up and down GEMMs
+#ifndef VM_GU_WAVES
+#define VM_GU_WAVES 4
+#endif
+#ifndef VM_GU_NBW
+#define VM_GU_NBW 1
+#endif
+#ifndef VM_DN_WAVES
+#define VM_DN_WAVES 4
+#endif
+#ifndef VM_DN_NBW
+#define VM_DN_NBW 2
+#endif
+
 hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
   switch (epi) {
-    case kEpiSwiglu: return grouped_go<kEpiSwiglu, 8, 1, 2>("grouped_gateup", p, max_tiles, stream);
-    case kEpiRows: return grouped_go<kEpiRows, 8, 2, 1>("grouped_down", p, max_tiles, stream);
+    case kEpiSwiglu:
+      return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>("grouped_gateup", p, max_tiles, stream);
+    case kEpiRows: return grouped_go<kEpiRows, VM_DN_WAVES, VM_DN_NBW, 1>("grouped_down", p, max_tiles, stream);
     default: return grouped_go<kEpiLogits, 4, 1, 1>("router_gemm", p, max_tiles, stream);
   }
 }

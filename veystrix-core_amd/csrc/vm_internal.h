@@ -82,7 +82,10 @@ struct DownLaunch {
 };
 
 // ---------------------------------------------------------- grouped path --
-constexpr int kGroupedRows = 64;          // rows per grouped GEMM tile
+#ifndef VM_GROUPED_ROWS
+#define VM_GROUPED_ROWS 64
+#endif
+constexpr int kGroupedRows = VM_GROUPED_ROWS;  // rows per grouped GEMM tile (16, 32, 48 or 64)
 constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
 enum : int { kEpiSwiglu = 0, kEpiRows = 1, kEpiLogits = 2 };
 
