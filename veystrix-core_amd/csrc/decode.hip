@@ -232,14 +232,50 @@ __device__ uint32_t rank_key(const GateKeys<A>& g, uint32_t r, uint32_t& above) 
 // so the K-th largest gate is at least the K-th largest lane maximum: every
 // gate >= that bound is a candidate.  When more than kMaxCand gates reach the
 // bound (many ties), the candidates are exactly the top K instead: the gates
-// above the K-th largest key plus the lowest-index ties at it.  Candidates go
-// to `cand` as (key << 32 | ~expert), which orders like (gate desc, index
-// asc).  Returns their number (K..kMaxCand).
+// above the K-th largest key plus the lowest-index ties at it.  A candidate is
+// stored as one key that orders like (gate desc, index asc): for bf16 gates
+// (key << 9 | (511 - expert)) in 32 bits, for fp32 gates (key << 32 | ~expert)
+// in 64 bits.  Returns their number (K..kMaxCand).
 constexpr uint32_t kMaxCand = 64;
 
 template <class A>
-__device__ __forceinline__ uint32_t compact_candidates(const GateKeys<A>& g, uint32_t bound, uint32_t need,
-                                                       uint32_t lane, uint64_t* cand) {
+struct Cand {
+  using T = typename std::conditional<is_bf16<A>(), uint32_t, uint64_t>::type;
+  __device__ static T make(uint32_t key, uint32_t expert) {
+    if constexpr (is_bf16<A>()) return (key << 9) | (511u - expert);
+    else return (static_cast<uint64_t>(key) << 32) | (0xffffffffu - expert);
+  }
+  __device__ static uint32_t expert(T c) {
+    if constexpr (is_bf16<A>()) return 511u - (c & 511u);
+    else return 0xffffffffu - static_cast<uint32_t>(c);
+  }
+  __device__ static uint32_t key(T c) {
+    if constexpr (is_bf16<A>()) return c >> 9;
+    else return static_cast<uint32_t>(c >> 32);
+  }
+};
+
+// First pass: every gate >= bound, in (m, lane) order.
+template <class A>
+__device__ __forceinline__ uint32_t compact_ge(const GateKeys<A>& g, uint32_t bound, uint32_t lane,
+                                               typename Cand<A>::T* cand) {
+  uint32_t c = 0;
+#pragma unroll
+  for (int m = 0; m < kMaxExpertsPerLane; ++m) {
+    const bool take = g.k[m] >= bound;
+    const uint64_t sel = __ballot(take);
+    const uint32_t pos = c + mbcnt(sel);
+    if (take && pos < kMaxCand) cand[pos] = Cand<A>::make(g.k[m], lane + 64u * m);
+    c += __popcll(sel);
+  }
+  return c;
+}
+
+// Exact top K when ties crowd the bound: the keys above `bound` and the
+// first `need` ties at it in index order.
+template <class A>
+__device__ uint32_t compact_top(const GateKeys<A>& g, uint32_t bound, uint32_t need, uint32_t lane,
+                                typename Cand<A>::T* cand) {
   uint32_t eq_before = 0, c = 0;
 #pragma unroll
   for (int m = 0; m < kMaxExpertsPerLane; ++m) {
@@ -248,29 +284,49 @@ __device__ __forceinline__ uint32_t compact_candidates(const GateKeys<A>& g, uin
     const bool take = k > bound || (k == bound && eq_before + mbcnt(eq) < need);
     const uint64_t sel = __ballot(take);
     const uint32_t pos = c + mbcnt(sel);
-    if (take && pos < kMaxCand)
-      cand[pos] = (static_cast<uint64_t>(k) << 32) | (0xffffffffu - (lane + 64u * m));
+    if (take && pos < kMaxCand) cand[pos] = Cand<A>::make(k, lane + 64u * m);
     eq_before += __popcll(eq);
     c += __popcll(sel);
   }
   return c;
 }
 
+// K-th largest lane maximum: a search over the key range that tests three
+// thresholds per step (independent ballots), two bits per step.
 template <class A>
-__device__ uint32_t gather_candidates(const GateKeys<A>& g, uint32_t K, uint32_t lane, uint64_t* cand) {
+__device__ __forceinline__ uint32_t kth_lane_max(uint32_t lmax, uint32_t K) {
+  uint32_t lo = 0, hi = GateKeys<A>::kTop + 1;  // count(lmax >= lo) >= K > count(lmax >= hi)
+  while (hi - lo > 1) {
+    const uint32_t q = (hi - lo + 3) >> 2;
+    const uint32_t m1 = lo + q, m2 = min(lo + 2 * q, hi), m3 = min(lo + 3 * q, hi);
+    const uint32_t c1 = __popcll(__ballot(lmax >= m1));
+    const uint32_t c2 = __popcll(__ballot(lmax >= m2));
+    const uint32_t c3 = __popcll(__ballot(lmax >= m3));
+    if (c3 >= K) {
+      lo = m3;
+    } else if (c2 >= K) {
+      lo = m2;
+      hi = m3;
+    } else if (c1 >= K) {
+      lo = m1;
+      hi = m2;
+    } else {
+      hi = m1;
+    }
+  }
+  return lo;
+}
+
+template <class A>
+__device__ uint32_t gather_candidates(const GateKeys<A>& g, uint32_t K, uint32_t lane, typename Cand<A>::T* cand) {
   uint32_t lmax = g.k[0];
 #pragma unroll
   for (int m = 1; m < kMaxExpertsPerLane; ++m) lmax = max(lmax, g.k[m]);
-  uint32_t lo = 0, hi = GateKeys<A>::kTop + 1;  // count(lmax >= lo) >= K > count(lmax >= hi)
-  while (hi - lo > 1) {
-    const uint32_t mid = (lo + hi) >> 1;
-    if (static_cast<uint32_t>(__popcll(__ballot(lmax >= mid))) >= K) lo = mid; else hi = mid;
-  }
-  uint32_t c = compact_candidates(g, lo, 0xffffffffu, lane, cand);
+  uint32_t c = compact_ge(g, kth_lane_max<A>(lmax, K), lane, cand);
   if (c > kMaxCand) {
     uint32_t above;
     const uint32_t vk = rank_key(g, K - 1, above);
-    c = compact_candidates(g, vk, K - above, lane, cand);
+    c = compact_top(g, vk, K - above, lane, cand);
   }
   __builtin_amdgcn_wave_barrier();
   return c;
@@ -278,7 +334,9 @@ __device__ uint32_t gather_candidates(const GateKeys<A>& g, uint32_t K, uint32_t
 
 // Rank of candidate `lane` among the c candidates (0 = largest gate); lanes
 // >= c get `mine` = 0.
-__device__ __forceinline__ uint32_t candidate_rank(const uint64_t* cand, uint32_t c, uint32_t lane, uint64_t& mine) {
+template <class A>
+__device__ __forceinline__ uint32_t candidate_rank(const typename Cand<A>::T* cand, uint32_t c, uint32_t lane,
+                                                   typename Cand<A>::T& mine) {
   mine = lane < c ? cand[lane] : 0u;
   uint32_t r = 0;
 #pragma unroll 4
@@ -288,13 +346,18 @@ __device__ __forceinline__ uint32_t candidate_rank(const uint64_t* cand, uint32_
 
 // Expert of rank r < K (wave-uniform).
 template <class A>
-__device__ uint32_t select_rank(const GateKeys<A>& g, uint32_t K, uint32_t r, uint32_t lane, uint64_t* cand) {
+__device__ uint32_t select_rank(const GateKeys<A>& g, uint32_t K, uint32_t r, uint32_t lane,
+                                typename Cand<A>::T* cand) {
   const uint32_t c = gather_candidates(g, K, lane, cand);
-  uint64_t mine;
-  const uint32_t rank = candidate_rank(cand, c, lane, mine);
+  typename Cand<A>::T mine;
+  const uint32_t rank = candidate_rank<A>(cand, c, lane, mine);
   const uint64_t hit = __ballot(lane < c && rank == r);
   const uint32_t src = static_cast<uint32_t>(__builtin_ctzll(hit));
-  return 0xffffffffu - static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine), src));
+  if constexpr (is_bf16<A>()) {
+    return Cand<A>::expert(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mine), src)));
+  } else {
+    return Cand<A>::expert(readlane_u64(mine, src));
+  }
 }
 
 // The whole selection in rank order: lane k < K returns the expert of rank k
@@ -302,27 +365,27 @@ __device__ uint32_t select_rank(const GateKeys<A>& g, uint32_t K, uint32_t r, ui
 // - mass)), each step rounded to the activation type; the mass is summed in
 // rank order.
 template <class A>
-__device__ void rank_selection(const GateKeys<A>& g, uint32_t K, float blend, uint32_t lane, uint64_t* cand,
-                               uint32_t& e_out, float& score_out) {
+__device__ void rank_selection(const GateKeys<A>& g, uint32_t K, float blend, uint32_t lane,
+                               typename Cand<A>::T* cand, uint32_t& e_out, float& score_out) {
   const uint32_t c = gather_candidates(g, K, lane, cand);
-  uint64_t mine;
-  const uint32_t rank = candidate_rank(cand, c, lane, mine);
+  typename Cand<A>::T mine;
+  const uint32_t rank = candidate_rank<A>(cand, c, lane, mine);
   __builtin_amdgcn_wave_barrier();
   if (lane < c && rank < K) cand[rank] = mine;
   __builtin_amdgcn_wave_barrier();
   float mass = 0.0f;
-  for (uint32_t i = 0; i < K; ++i) mass += GateKeys<A>::gate(static_cast<uint32_t>(cand[i] >> 32));
+  for (uint32_t i = 0; i < K; ++i) mass += GateKeys<A>::gate(Cand<A>::key(cand[i]));
   mass = A::round(mass);
   const float diff = A::round(mass - mass);
   const float normalizer = A::round(mass + A::round(blend * diff));
-  const uint64_t top = lane < K ? cand[lane] : 0u;
-  e_out = lane < K ? 0xffffffffu - static_cast<uint32_t>(top) : 0u;
-  score_out = lane < K ? A::round(GateKeys<A>::gate(static_cast<uint32_t>(top >> 32)) / normalizer) : 0.0f;
+  const typename Cand<A>::T top = lane < K ? cand[lane] : 0u;
+  e_out = lane < K ? Cand<A>::expert(top) : 0u;
+  score_out = lane < K ? A::round(GateKeys<A>::gate(Cand<A>::key(top)) / normalizer) : 0.0f;
 }
 
 template <class A>
 __device__ void select_body(const SelectLaunch& p) {
-  __shared__ uint64_t s_cand[kMaxCand];
+  __shared__ typename Cand<A>::T s_cand[kMaxCand];
   const uint32_t t = blockIdx.x;
   const uint32_t lane = threadIdx.x;
   GateKeys<A> g;
@@ -465,22 +528,6 @@ __device__ __forceinline__ uint32_t route_word(int32_t slot) {
   return slot >= 0 ? (kSlotBit | static_cast<uint32_t>(slot)) : kMissWord;
 }
 
-__device__ __forceinline__ void pin_proj(const ProjPtrs& q) {
-  VM_PIN(q.w);
-  VM_PIN(q.s);
-  VM_PIN(q.b);
-}
-
-template <int FIRST, int PARTS>
-__device__ __forceinline__ void pin_view(const PoolDev& v) {
-  VM_PIN(v.base);
-  VM_PIN(v.header);
-  VM_PIN(v.stride);
-  VM_PIN(v.records);
-#pragma unroll
-  for (int i = 0; i < PARTS; ++i) VM_PIN(v.off[FIRST + i]);
-}
-
 // SwiGLU of one row and the optional raw gate/up outputs.
 template <class A>
 __device__ __forceinline__ void gateup_store(const GateUpLaunch& p, uint32_t t, uint32_t j, uint32_t S, bool routed,
@@ -504,7 +551,7 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
   constexpr int RPW = RPI * U;
   constexpr int RPB = RPW * kWaves;
   __shared__ uint32_t s_word;
-  __shared__ uint64_t s_cand[kMaxCand];
+  __shared__ typename Cand<A>::T s_cand[kMaxCand];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
@@ -517,11 +564,20 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
   const uint32_t t = shared_pair ? pair - routed_pairs : pair / p.slots;
   const uint32_t j = shared_pair ? p.slots : pair % p.slots;
   const uint32_t S = p.slots + p.has_shared;
-  const uint32_t H = p.hidden, I = p.inter, G = H / kGroup, E = p.experts;
+  const uint32_t H = p.hidden, I = p.inter, G = H / kGroup;
+  uint32_t E = p.experts;
   const bool select = !shared_pair && p.logits != nullptr;
   PhaseTrace tr;
   if (p.trace != nullptr) tr.mark(0);
-  pin_view<0, 6>(p.pool);
+  // the arguments used after the selection, held in SGPRs from here on (the
+  // stream view serves split-phase routes only and is read where it is used)
+  PoolDev pool = p.pool;
+  const PoolDev& stream = p.stream;
+  keep_view<0, 6>(pool);
+  ProjPtrs gate = p.gate, up = p.up;
+  keep_proj(gate);
+  keep_proj(up);
+  VM_KEEP(E);
   VM_PIN(p.act);
 
   // 1. loads: the selection's logits and slot-table entries first, then this
@@ -577,11 +633,11 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
     upp = p.shared_up;
   } else {
     uint32_t index = 0;
-    const int kind = resolve_word(word, select ? nullptr : p.slot_table, E, p.pool, &p.stream,
-                                  p.gate.w != nullptr && p.up.w != nullptr, index);
+    const int kind = resolve_word(word, select ? nullptr : p.slot_table, E, pool, &stream,
+                                  gate.w != nullptr && up.w != nullptr, index);
     ok = kind != kSrcNone;
-    source_proj(kind, index, p.pool, &p.stream, p.gate, 0, I, H, gp);
-    source_proj(kind, index, p.pool, &p.stream, p.up, 1, I, H, upp);
+    source_proj(kind, index, pool, &stream, gate, 0, I, H, gp);
+    source_proj(kind, index, pool, &stream, up, 1, I, H, upp);
   }
   if (!ok && tid == 0 && blockIdx.x == 0) flag(p.status, 1u);
   if (p.trace != nullptr) tr.mark(1);
@@ -695,8 +751,14 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   const uint32_t row0 = blockIdx.x * RB;
   PhaseTrace tr;
   if (p.trace != nullptr) tr.mark(0);
-  pin_view<6, 3>(p.pool);
-  pin_proj(p.shared_down);
+  PoolDev pool = p.pool;
+  const PoolDev& stream = p.stream;
+  keep_view<6, 3>(pool);
+  ProjPtrs down = p.down, shared_down = p.shared_down;
+  keep_proj(down);
+  keep_proj(shared_down);
+  uint32_t E = p.experts;
+  VM_KEEP(E);
   VM_PIN(p.act);
 
   // 1. loads: the route words first (lane k < K reads slot k), then this
@@ -711,14 +773,31 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
     xa[i].fetch(live ? p.act : g_zero_page, live ? (static_cast<size_t>(t) * S + slot) * I + lr * kGroup : 0);
   }
 
+  // epilogue operands as raw bits: loaded now, converted into LDS after the
+  // weight loads are issued, so no load waits in front of those
+  const bool combine = p.scores != nullptr;
+  const uint32_t er = tid - 64;  // wave 1 fetches the shared term of the tile
+  const void* sh_src = p.shared_y != nullptr ? p.shared_y : p.shared;
+  const bool take_score = combine && tid < K;
+  const bool take_shared = combine && tid >= 64 && er < RB && row0 + er < H && sh_src != nullptr;
+  const void* sig_src = p.has_shared ? p.shared_sig : p.shared != nullptr ? p.shared_gate : nullptr;
+  const bool take_sig = combine && tid == 128 && sig_src != nullptr;
+  uint32_t r_score = 0, r_shared = 0, r_sig = 0;
+  if (take_score) {
+    const size_t o = static_cast<size_t>(t) * K + tid;
+    r_score = p.score_dtype == 0 ? ldg_u16(static_cast<const uint16_t*>(p.scores) + o)
+                                 : ldg_u32(static_cast<const uint32_t*>(p.scores) + o);
+  }
+  if (take_shared) r_shared = A::load_bits(sh_src, static_cast<size_t>(t) * H + row0 + er);
+  if (take_sig) r_sig = A::load_bits(sig_src, t);
+
   // 2. lane k < K resolves slot k; the waves take their slots' pointers with
   //    readlane and issue their weight loads
   ProjPtrs mine{};
   uint32_t index = 0;
-  const int kind = lane < K ? resolve_word(route, p.slot_table, p.experts, p.pool, &p.stream, p.down.w != nullptr,
-                                           index)
+  const int kind = lane < K ? resolve_word(route, p.slot_table, E, pool, &stream, down.w != nullptr, index)
                             : kSrcNone;
-  source_proj(kind, index, p.pool, &p.stream, p.down, 2, H, I, mine);
+  source_proj(kind, index, pool, &stream, down, 2, H, I, mine);
   const bool mine_ok = kind != kSrcNone;
   if (!mine_ok && lane < K && wave == 0 && blockIdx.x == 0) flag(p.status, 1u);
   const uint64_t ok_mask = __ballot(mine_ok);
@@ -730,18 +809,16 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   const size_t row_words = I / 8;
 #pragma unroll
   for (int i = 0; i < kDownSlotsPerWave; ++i) {
+    // no branch around the loads: slots past S load zeros, so the first use
+    // of the data, not its load, waits
     const uint32_t slot = wave + kWaves * i;
-    if (slot >= S) break;  // wave-uniform
-    ProjPtrs dp{};
-    bool ok;
+    ProjPtrs dp = shared_down;
+    bool ok = slot < S;
     if (slot < K) {
       ok = (ok_mask >> slot) & 1u;
       dp.w = reinterpret_cast<const uint32_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.w), slot));
       dp.s = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.s), slot));
       dp.b = reinterpret_cast<const uint16_t*>(readlane_u64(reinterpret_cast<uint64_t>(mine.b), slot));
-    } else {
-      dp = p.shared_down;
-      ok = true;
     }
 #pragma unroll
     for (int q = 0; q < kDownQuads; ++q) {
@@ -755,20 +832,10 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   }
   if (p.trace != nullptr) tr.mark(6);
 
-  // 3. epilogue operands
-  if (p.scores != nullptr) {
-    if (tid < K) s_scores[tid] = load_any(p.scores, static_cast<size_t>(t) * K + tid, p.score_dtype);
-    const uint32_t r = tid - 64;  // wave 1 fetches the shared term of the tile
-    if (tid >= 64 && r < RB && row0 + r < H) {
-      const size_t o = static_cast<size_t>(t) * H + row0 + r;
-      if (p.shared_y != nullptr) s_shared[r] = A::load(p.shared_y, o);
-      else if (p.shared != nullptr) s_shared[r] = A::load(p.shared, o);
-    }
-    if (tid == 128) {
-      if (p.has_shared) s_sig = A::load(p.shared_sig, t);
-      else if (p.shared != nullptr) s_sig = A::load(p.shared_gate, t);
-    }
-  }
+  // 3. epilogue operands into LDS
+  if (take_score) s_scores[tid] = p.score_dtype == 0 ? bf16_to_f32(r_score) : __uint_as_float(r_score);
+  if (take_shared) s_shared[er] = A::from_bits(r_shared);
+  if (take_sig) s_sig = A::from_bits(r_sig);
   if (p.trace != nullptr) tr.mark(7);
 
   // 4. dot products and row sums into LDS

@@ -39,6 +39,9 @@ struct ActBF16 {
   __device__ static __forceinline__ void store(void* p, size_t i, float v) {
     static_cast<uint16_t*>(p)[i] = static_cast<uint16_t>(f32_to_bf16(v));
   }
+  // raw element bits (the conversion, and so the wait, comes at from_bits)
+  __device__ static __forceinline__ uint32_t load_bits(const void* p, size_t i);
+  __device__ static __forceinline__ float from_bits(uint32_t b) { return bf16_to_f32(b); }
 };
 
 struct ActF32 {
@@ -51,6 +54,8 @@ struct ActF32 {
   __device__ static __forceinline__ void store(void* p, size_t i, float v) {
     static_cast<float*>(p)[i] = v;
   }
+  __device__ static __forceinline__ uint32_t load_bits(const void* p, size_t i);
+  __device__ static __forceinline__ float from_bits(uint32_t b) { return __uint_as_float(b); }
 };
 
 __device__ __forceinline__ float load_any(const void* p, size_t i, uint32_t dtype) {
@@ -77,10 +82,21 @@ __device__ __forceinline__ uint32_t ldg_u32(const void* p) {
   return *(const __attribute__((address_space(1))) unsigned int*)(p);
 }
 
+__device__ __forceinline__ uint32_t ActBF16::load_bits(const void* p, size_t i) {
+  return ldg_u16(static_cast<const uint16_t*>(p) + i);
+}
+__device__ __forceinline__ uint32_t ActF32::load_bits(const void* p, size_t i) {
+  return ldg_u32(static_cast<const float*>(p) + i);
+}
+
 // Materialises a kernel-argument value in SGPRs at this point.  Members of a
 // by-value kernel argument are otherwise read at their first use, which puts
 // one scalar-load round trip per use on the critical path.
 #define VM_PIN(value) asm volatile("" ::"s"(value))
+
+// Keeps a uniform local copy of a kernel-argument value in SGPRs: after this
+// the compiler cannot re-read it from the argument segment at a later use.
+#define VM_KEEP(lvalue) asm volatile("" : "+s"(lvalue))
 
 // ---------------------------------------------------------- activations --
 // MLX's stable sigmoid sequence, every step rounded to the activation type
@@ -249,6 +265,23 @@ struct PoolDev {
   uint64_t off[9];
   uint32_t records;
 };
+
+__device__ __forceinline__ void keep_proj(ProjPtrs& q) {
+  VM_KEEP(q.w);
+  VM_KEEP(q.s);
+  VM_KEEP(q.b);
+}
+
+// Local SGPR copy of parts [FIRST, FIRST + PARTS) of a pool view (VM_KEEP).
+template <int FIRST, int PARTS>
+__device__ __forceinline__ void keep_view(PoolDev& v) {
+  VM_KEEP(v.base);
+  VM_KEEP(v.header);
+  VM_KEEP(v.stride);
+  VM_KEEP(v.records);
+#pragma unroll
+  for (int i = 0; i < PARTS; ++i) VM_KEEP(v.off[FIRST + i]);
+}
 
 __device__ __forceinline__ void record_parts(const PoolDev& view, uint32_t record, int proj, ProjPtrs& out) {
   const uint8_t* rec = view.base + view.header + static_cast<uint64_t>(record) * view.stride;
