@@ -48,6 +48,11 @@ constexpr int kWaves = kBlock / 64;
 #define VM_DOWN_QUADS 2
 #endif
 constexpr int kGateupRowsPerLane = VM_GATEUP_ROWS;
+#ifndef VM_GATEUP_WAVES
+#define VM_GATEUP_WAVES 2
+#endif
+constexpr int kGuWaves = VM_GATEUP_WAVES;  // waves per gate/up block
+constexpr int kGuBlock = kGuWaves * 64;
 constexpr int kMaxExpertsPerLane = 8;  // expert_count <= 512
 
 template <class A>
@@ -546,10 +551,10 @@ __device__ __forceinline__ void gateup_store(const GateUpLaunch& p, uint32_t t, 
 // LPR lanes per row (one 32-input group per lane and iteration, GI
 // iterations), U rows per lane group; a block covers RPB = (64/LPR)*U*4 rows.
 template <class A, int LPR, int GI, int U>
-__global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
+__global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RPW = RPI * U;
-  constexpr int RPB = RPW * kWaves;
+  constexpr int RPB = RPW * kGuWaves;
   __shared__ uint32_t s_word;
   __shared__ typename Cand<A>::T s_cand[kMaxCand];
 
@@ -725,13 +730,18 @@ __global__ __launch_bounds__(kBlock) void k_gateup(GateUpLaunch p) {
 // ----------------------------------------------------------------- down ---
 
 constexpr int kDownMaxSlots = 12;                         // MAX_TOP_K (10) + shared, rounded up
-constexpr int kDownSlotsPerWave = kDownMaxSlots / kWaves;  // wave w owns slots w, w+4, w+8
+#ifndef VM_DOWN_WAVES
+#define VM_DOWN_WAVES 8
+#endif
+constexpr int kDownWaves = VM_DOWN_WAVES;                  // waves per down block
+constexpr int kDownBlock = kDownWaves * 64;
+constexpr int kDownSlotsPerWave = (kDownMaxSlots + kDownWaves - 1) / kDownWaves;  // wave w owns slots w + kDownWaves i
 constexpr int kDownQuads = VM_DOWN_QUADS;                 // row groups of 64/LPR rows per block
 
 // LPR = I/32 lanes per row (one group each); a block covers RB rows of all
 // slots of one token.
 template <class A, int LPR>
-__global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
+__global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RB = RPI * kDownQuads;
   __shared__ float s_part[kDownMaxSlots * RB];
@@ -768,7 +778,7 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   GroupAct<A> xa[kDownSlotsPerWave];
 #pragma unroll
   for (int i = 0; i < kDownSlotsPerWave; ++i) {
-    const uint32_t slot = wave + kWaves * i;
+    const uint32_t slot = wave + kDownWaves * i;
     const bool live = slot < S && lr < G;
     xa[i].fetch(live ? p.act : g_zero_page, live ? (static_cast<size_t>(t) * S + slot) * I + lr * kGroup : 0);
   }
@@ -811,7 +821,7 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   for (int i = 0; i < kDownSlotsPerWave; ++i) {
     // no branch around the loads: slots past S load zeros, so the first use
     // of the data, not its load, waits
-    const uint32_t slot = wave + kWaves * i;
+    const uint32_t slot = wave + kDownWaves * i;
     ProjPtrs dp = shared_down;
     bool ok = slot < S;
     if (slot < K) {
@@ -841,7 +851,7 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
   // 4. dot products and row sums into LDS
 #pragma unroll
   for (int i = 0; i < kDownSlotsPerWave; ++i) {
-    const uint32_t slot = wave + kWaves * i;
+    const uint32_t slot = wave + kDownWaves * i;
     if (slot >= S) break;  // wave-uniform
     xa[i].prepare();
 #pragma unroll
@@ -875,7 +885,7 @@ __global__ __launch_bounds__(kBlock) void k_down(DownLaunch p) {
       A::store(p.out, static_cast<size_t>(t) * H + row0 + r, y);
     }
   } else {
-    for (uint32_t idx = tid; idx < K * RB; idx += kBlock) {
+    for (uint32_t idx = tid; idx < K * RB; idx += kDownBlock) {
       const uint32_t k = idx / RB, r = idx % RB;
       if (row0 + r < H) A::store(p.out, (static_cast<size_t>(t) * K + k) * H + row0 + r, A::round(s_part[k * RB + r]));
     }
@@ -926,12 +936,12 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
 
 template <class A, int LPR, int GI, int U>
 hipError_t gateup_go(const GateUpLaunch& p, hipStream_t stream) {
-  constexpr int RPB = (64 / LPR) * U * kWaves;
+  constexpr int RPB = (64 / LPR) * U * kGuWaves;
   const uint32_t pairs = p.tokens * p.slots + (p.has_shared ? p.tokens : 0);
   dim3 grid((p.inter + RPB - 1) / RPB, pairs);
   GateUpLaunch q = p;
   q.trace = trace_reserve(grid.x * grid.y);
-  return launch("gateup", k_gateup<A, LPR, GI, U>, grid, dim3(kBlock), stream, q);
+  return launch("gateup", k_gateup<A, LPR, GI, U>, grid, dim3(kGuBlock), stream, q);
 }
 
 template <class A>
@@ -959,7 +969,7 @@ hipError_t down_go(const DownLaunch& p, hipStream_t stream) {
   dim3 grid((p.hidden + RB - 1) / RB, p.tokens);
   DownLaunch q = p;
   q.trace = trace_reserve(grid.x * grid.y);
-  return launch("down", k_down<A, LPR>, grid, dim3(kBlock), stream, q);
+  return launch("down", k_down<A, LPR>, grid, dim3(kDownBlock), stream, q);
 }
 
 template <class A>
