@@ -192,6 +192,8 @@ class MoELayer:
         self.last_scores = None
         self._ws = {}
         self._args_cache = {}
+        self._route_host = None   # pinned host copy of the routed ids (split-phase path)
+        self._route_event = None
 
     @property
     def hidden(self) -> int:
@@ -269,7 +271,7 @@ class MoELayer:
             # router, then the host LRU pass on synced routes, then the experts
             args.phases = _lib.VM_PHASE_ROUTER
             _lib.check(lib.vm_moe_layer(args, stream_handle()))
-            routed = inds.reshape(-1).tolist()
+            routed = self._routes_to_host(inds)
             wanted = list(dict.fromkeys(routed))
             slots, misses = sw.pool.assign(sw.layer_id, wanted)
             sw.hits += len(routed) - len(misses)
@@ -284,6 +286,19 @@ class MoELayer:
         _lib.check(lib.vm_moe_layer(args, stream_handle()))
         self.last_inds, self.last_scores = inds, scores
         return out
+
+    def _routes_to_host(self, inds: torch.Tensor) -> list:
+        """The routed expert ids on the host: one D2H copy into a pinned
+        buffer kept per layer, then a wait on its event."""
+        n = inds.numel()
+        host = self._route_host
+        if host is None or host.numel() != n:
+            host = self._route_host = torch.empty(n, dtype=torch.int32, pin_memory=True)
+            self._route_event = torch.cuda.Event()
+        host.copy_(inds.reshape(-1), non_blocking=True)
+        self._route_event.record()
+        self._route_event.synchronize()
+        return host.tolist()
 
     decode = forward
     prefill = forward

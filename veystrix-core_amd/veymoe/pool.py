@@ -90,7 +90,9 @@ class ExpertPool:
         self.bytes_staged = 0
         self._copy_stream = None
         self._pinned_table = None
-        self._table_event = None
+        self._row_events = {}      # layer -> event after the last upload of its pinned row
+        self._stage_events = None  # (compute reached the copies, copies done), reused
+        self._stage_args = None    # ctypes index arrays, grown on demand
 
     @classmethod
     def from_bytes(cls, layout: RecordLayout, size_bytes: int, **kwargs):
@@ -175,20 +177,23 @@ class ExpertPool:
     def sync_tables(self) -> None:
         """Upload the slot-table rows changed since the last call, asynchronously
         on the current stream (ordered before any kernel launched after it),
-        from a pinned mirror that is not rewritten before the last upload ran."""
+        from a pinned mirror row that is rewritten only after its last upload
+        ran (one event per row, normally complete by then)."""
         if not self._dirty:
             return
         if self._pinned_table is None:
             self._pinned_table = torch.empty((self.layers, self.experts), dtype=torch.int32,
                                              pin_memory=self.device.type == "cuda")
-        if self._table_event is not None:
-            self._table_event.synchronize()
         stream = torch.cuda.current_stream(self.device)
         for layer in sorted(self._dirty):
+            event = self._row_events.get(layer)
+            if event is None:
+                event = self._row_events[layer] = torch.cuda.Event()
+            elif not event.query():
+                event.synchronize()
             self._pinned_table[layer].numpy()[:] = self._host_table[layer]
             self.slot_table[layer].copy_(self._pinned_table[layer], non_blocking=True)
-        self._table_event = torch.cuda.Event()
-        self._table_event.record(stream)
+            event.record(stream)
         self._dirty.clear()
 
     def place(self, layer: int, expert: int, slot: int) -> None:
@@ -230,28 +235,38 @@ class ExpertPool:
 
     def stage(self, source: HostRecordStore, layer: int, misses, compute_stream=None) -> torch.cuda.Event | None:
         """Copy the records of ``misses`` [(expert, slot)] from pinned host memory
-        into their slots on the side stream; the compute stream waits for it."""
+        into their slots on the side stream; the compute stream waits for it.
+        Returns the completion event, which the next call records again."""
         if not misses:
             return None
         order = sorted(misses, key=lambda item: item[1])
-        src = (ctypes.c_int64 * len(order))(*[source.row(layer, e) for e, _ in order])
-        dst = (ctypes.c_int64 * len(order))(*[slot for _, slot in order])
+        n = len(order)
+        if self._stage_args is None or len(self._stage_args[0]) < n:
+            size = max(64, n)
+            self._stage_args = ((ctypes.c_int64 * size)(), (ctypes.c_int64 * size)())
+        src, dst = self._stage_args
+        for i, (expert, slot) in enumerate(order):
+            src[i] = source.row(layer, expert)
+            dst[i] = slot
         compute = torch.cuda.current_stream(self.device) if compute_stream is None else compute_stream
         copier = self.copy_stream()
+        if self._stage_events is None:
+            self._stage_events = (torch.cuda.Event(), torch.cuda.Event())
+        reached, done = self._stage_events
         # a slot may still be read by kernels queued before this point
-        copier.wait_stream(compute)
+        reached.record(compute)
+        copier.wait_event(reached)
         rc = _lib.lib().vm_pool_stage(
             self.buffer.data_ptr(), self.header_size, self.stride, self.slots,
             source.buffer.data_ptr(), source.layout.record_stride, source.capacity,
-            self.layout.record_bytes, src, dst, len(order), stream_handle(copier))
+            self.layout.record_bytes, src, dst, n, stream_handle(copier))
         if rc != _lib.VM_OK:
             self.invalidate(layer, misses)
             _lib.check(rc)
-        event = torch.cuda.Event()
-        event.record(copier)
-        compute.wait_event(event)
-        self.bytes_staged += len(order) * self.layout.record_bytes
-        return event
+        done.record(copier)
+        compute.wait_event(done)
+        self.bytes_staged += n * self.layout.record_bytes
+        return done
 
     def fill(self, layer: int, misses, source: HostRecordStore, compute_stream=None):
         """Stage misses; on any failure invalidate them before re-raising."""
