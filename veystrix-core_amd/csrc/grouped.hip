@@ -83,9 +83,8 @@ __device__ __forceinline__ uint32_t f16_magic() {
 // (s/16)*(1024 + 16 q) + (b - 64 s) for the high one.
 struct Dequant {
   float s, b1024, s16, b64;
-  __device__ __forceinline__ Dequant(uint32_t s_bits, uint32_t b_bits) {
-    s = bf16_to_f32(s_bits);
-    const float b = bf16_to_f32(b_bits);
+  __device__ __forceinline__ Dequant(float scale, float b) {
+    s = scale;
     b1024 = fmaf(-1024.0f, s, b);
     s16 = 0.0625f * s;
     b64 = fmaf(-64.0f, s, b);
@@ -121,32 +120,47 @@ __device__ __forceinline__ bf16x8_t as_operand(const uint32_t r[4]) {
 // B side of one lane for one chunk: groups g0 + 4 h + kb (h < kHalves) of
 // one weight row, Q4 (16 bytes + scale + bias each) or bf16 (32 weights each).
 // Chunk step st uses half st/4, packed word st%4.
-template <bool Q4>
+template <bool Q4, bool TAIL>
 struct BChunk;
 
+// Q4, full chunk: one 16-byte load brings the scales (one the biases) of the
+// chunk's eight groups of this lane's row; a per-lane byte permute picks the
+// lane's two groups out of them (kb and 4 + kb) as fp32 bit patterns.
 template <>
-struct BChunk<true> {
+struct BChunk<true, false> {
+  static_assert(kCG == 8, "the scale vector covers eight groups");
+  uint4 w[kHalves];
+  uint4 sv, bv;
+  __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t mrow, uint32_t g0, uint32_t kb,
+                                       uint32_t, bool) {
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.w) + g0 * 16u;
+    const uint32_t wl = wrow + kb * 16u;
+#pragma unroll
+    for (int h = 0; h < kHalves; ++h) w[h] = ldg16(wb + wl + h * 64u);
+    sv = ldg16(reinterpret_cast<const uint8_t*>(p.s) + g0 * 2u + mrow);
+    bv = ldg16(reinterpret_cast<const uint8_t*>(p.b) + g0 * 2u + mrow);
+  }
+  // sel: bytes (2 kb, 2 kb + 1) of a dword pair into the high half
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t sel) const {
+    const int h = st >> 2, i = st & 3;
+    const float sc = __uint_as_float(__builtin_amdgcn_perm(h ? sv.w : sv.y, h ? sv.z : sv.x, sel));
+    const float bi = __uint_as_float(__builtin_amdgcn_perm(h ? bv.w : bv.y, h ? bv.z : bv.x, sel));
+    const Dequant dq(sc, bi);
+    const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
+    uint32_t r[4];
+    dq.word(word, magic, r);
+    return as_operand(r);
+  }
+};
+
+// Q4, tail chunk: groups past the end are clamped (their activations are
+// staged as zeros); scales and biases one by one.
+template <>
+struct BChunk<true, true> {
   uint4 w[kHalves];
   uint32_t s[kHalves], b[kHalves];
-  // p: the projection (uniform), wrow/mrow: byte offsets of this lane's row in
-  // the packed words / the scales and biases.  A chunk inside the row takes
-  // uniform chunk offsets (no per-lane address arithmetic); in the tail chunk
-  // groups past the end are clamped (their activations are staged as zeros).
   __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t mrow, uint32_t g0, uint32_t kb,
-                                       uint32_t G, bool tail) {
-    if (!tail) {
-      const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.w) + g0 * 16u;
-      const uint8_t* sb = reinterpret_cast<const uint8_t*>(p.s) + g0 * 2u;
-      const uint8_t* bb = reinterpret_cast<const uint8_t*>(p.b) + g0 * 2u;
-      const uint32_t wl = wrow + kb * 16u, ml = mrow + kb * 2u;
-#pragma unroll
-      for (int h = 0; h < kHalves; ++h) {
-        w[h] = ldg16(wb + wl + h * 64u);
-        s[h] = ldg_u16(sb + ml + h * 8u);
-        b[h] = ldg_u16(bb + ml + h * 8u);
-      }
-      return;
-    }
+                                       uint32_t G, bool) {
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) {
       const uint32_t g = min(g0 + 4 * h + kb, G - 1);
@@ -155,9 +169,9 @@ struct BChunk<true> {
       b[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.b) + mrow + g * 2u);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t) const {
     const int h = st >> 2, i = st & 3;
-    const Dequant dq(s[h], b[h]);
+    const Dequant dq(bf16_to_f32(s[h]), bf16_to_f32(b[h]));
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
     uint32_t r[4];
     dq.word(word, magic, r);
@@ -165,8 +179,8 @@ struct BChunk<true> {
   }
 };
 
-template <>
-struct BChunk<false> {
+template <bool TAIL>
+struct BChunk<false, TAIL> {
   uint4 v[kHalves][4];
   // router: bf16 weights [N, K]; wrow = byte offset of the row
   __device__ __forceinline__ void load(const uint16_t* wbf, uint32_t wrow, uint32_t, uint32_t g0, uint32_t kb,
@@ -179,7 +193,7 @@ struct BChunk<false> {
       for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 16 * i);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st, uint32_t) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t, uint32_t) const {
     uint32_t r[4];
     permute_word(v[st >> 2][st & 3], r);
     return as_operand(r);
@@ -247,6 +261,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   // B: lane -> (column lane%16 of each block, group g0 + lane/16); columns
   // past N read the last row and are not stored
   const uint32_t bn = lane & 15u, bkb = lane >> 4;
+  const uint32_t sel = 0x0c0cu | ((2u * bkb) << 16) | ((2u * bkb + 1u) << 24);
   uint32_t wrow[NBW], mrow[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
@@ -254,8 +269,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     wrow[nb] = Q4 ? col * (K / 2) : col * K * 2;
     mrow[nb] = col * G * 2;
   }
-  BChunk<Q4> b0[PROJ][NBW], b1[PROJ][NBW];
-  auto b_load = [&](BChunk<Q4> (&dst)[PROJ][NBW], uint32_t g0, bool tail) {
+  BChunk<Q4, TAIL> b0[PROJ][NBW], b1[PROJ][NBW];
+  auto b_load = [&](BChunk<Q4, TAIL> (&dst)[PROJ][NBW], uint32_t g0, bool tail) {
 #pragma unroll
     for (int pj = 0; pj < PROJ; ++pj) {
 #pragma unroll
@@ -278,7 +293,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   const uint32_t magic = Q4 ? f16_magic() : 0u;
   const uint32_t am = lane & 15u, akb = lane >> 4;
   const uint32_t a_lane = am * kRowBytes + akb * 64;
-  auto compute = [&](int buf, const BChunk<Q4> (&bc)[PROJ][NBW]) {
+  auto compute = [&](int buf, const BChunk<Q4, TAIL> (&bc)[PROJ][NBW]) {
     const uint8_t* s_a = s_a0 + buf * kStageBytes + a_lane;
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
@@ -291,7 +306,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-          const bf16x8_t bop = bc[pj][nb].step(st, magic);
+          const bf16x8_t bop = bc[pj][nb].step(st, magic, sel);
 #pragma unroll
           for (int mb = 0; mb < MBU; ++mb)
             acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
@@ -452,7 +467,12 @@ __device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
 // The whole sort in one block: LDS histogram of the routes, scan into row
 // offsets and the tile list (group, first row) of kBM-row tiles, LDS cursors,
 // scatter.  groups = experts (+1 for the shared rows) <= 1024.
+// BATCH pair ids per thread are loaded together (clamped, unconditional), so
+// each batch costs one load latency rather than one per pair; small calls use
+// BATCH = 1 (no clamped duplicates).
+template <int BATCH>
 __global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
+  constexpr int kSortBatch = BATCH;
   __shared__ uint32_t s_count[1024];
   __shared__ uint32_t s_wave[16];
   __shared__ uint32_t s_shared_first;
@@ -461,10 +481,19 @@ __global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
   const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
   s_count[g] = 0;
   __syncthreads();
-  for (uint32_t i = g; i < pairs; i += 1024) {
-    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
-    if (e < p.experts) atomicAdd(&s_count[e], 1u);
-    else flag(p.status, 2u);
+  auto load_batch = [&](uint32_t base, uint32_t (&e)[kSortBatch]) {
+#pragma unroll
+    for (int j = 0; j < kSortBatch; ++j) e[j] = static_cast<uint32_t>(p.inds[min(base + j * 1024 + g, pairs - 1)]);
+  };
+  for (uint32_t base = 0; base < pairs; base += 1024 * kSortBatch) {
+    uint32_t e[kSortBatch];
+    load_batch(base, e);
+#pragma unroll
+    for (int j = 0; j < kSortBatch; ++j) {
+      if (base + j * 1024 + g >= pairs) continue;
+      if (e[j] < p.experts) atomicAdd(&s_count[e[j]], 1u);
+      else flag(p.status, 2u);
+    }
   }
   __syncthreads();
   uint32_t n = 0;
@@ -485,14 +514,20 @@ __global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
   if (g == p.experts) s_shared_first = row_begin;
   s_count[g] = row_begin;  // scatter cursors
   __syncthreads();
-  for (uint32_t i = g; i < pairs; i += 1024) {
-    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
-    if (e < p.experts) {
-      const uint32_t pos = atomicAdd(&s_count[e], 1u);
-      p.row_token[pos] = i / p.slots;
-      p.pair_row[i] = pos;
-    } else {
-      p.pair_row[i] = kNoRow;
+  for (uint32_t base = 0; base < pairs; base += 1024 * kSortBatch) {
+    uint32_t e[kSortBatch];
+    load_batch(base, e);
+#pragma unroll
+    for (int j = 0; j < kSortBatch; ++j) {
+      const uint32_t i = base + j * 1024 + g;
+      if (i >= pairs) continue;
+      if (e[j] < p.experts) {
+        const uint32_t pos = atomicAdd(&s_count[e[j]], 1u);
+        p.row_token[pos] = i / p.slots;
+        p.pair_row[i] = pos;
+      } else {
+        p.pair_row[i] = kNoRow;
+      }
     }
   }
   for (uint32_t i = g; i < p.shared_rows; i += 1024) p.row_token[s_shared_first + i] = i;
@@ -651,7 +686,8 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
 }
 
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
-  return launch("sort", k_sort, dim3(1), dim3(1024), stream, p);
+  if (p.tokens * p.slots > 16384) return launch("sort", k_sort<16>, dim3(1), dim3(1024), stream, p);
+  return launch("sort", k_sort<1>, dim3(1), dim3(1024), stream, p);
 }
 
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {
