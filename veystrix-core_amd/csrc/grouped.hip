@@ -51,6 +51,14 @@ constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
 constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
 constexpr int kStageBytes = kBM * kRowBytes;
 
+// Bytes of one LDS stage of a grouped GEMM instance: the A rows, then for Q4
+// weights without a tail chunk the chunk's scale and bias vectors of every
+// column of the block (16 bytes each).
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+constexpr int stage_bytes() {
+  return kStageBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0);
+}
+
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -123,28 +131,25 @@ __device__ __forceinline__ bf16x8_t as_operand(const uint32_t r[4]) {
 template <bool Q4, bool TAIL>
 struct BChunk;
 
-// Q4, full chunk: one 16-byte load brings the scales (one the biases) of the
-// chunk's eight groups of this lane's row; a per-lane byte permute picks the
-// lane's two groups out of them (kb and 4 + kb) as fp32 bit patterns.
+// Q4, full chunk: the weights only.  The chunk's scales and biases are
+// staged in LDS with the activations (one 16-byte load per row for the whole
+// block, pair-permuted so that lane kb finds its groups kb and 4 + kb in one
+// dword each) and come into step() as bf16 pairs.
 template <>
 struct BChunk<true, false> {
-  static_assert(kCG == 8, "the scale vector covers eight groups");
   uint4 w[kHalves];
-  uint4 sv, bv;
-  __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t mrow, uint32_t g0, uint32_t kb,
+  __device__ __forceinline__ void load(const ProjPtrs& p, uint32_t wrow, uint32_t, uint32_t g0, uint32_t kb,
                                        uint32_t, bool) {
     const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.w) + g0 * 16u;
     const uint32_t wl = wrow + kb * 16u;
 #pragma unroll
     for (int h = 0; h < kHalves; ++h) w[h] = ldg16(wb + wl + h * 64u);
-    sv = ldg16(reinterpret_cast<const uint8_t*>(p.s) + g0 * 2u + mrow);
-    bv = ldg16(reinterpret_cast<const uint8_t*>(p.b) + g0 * 2u + mrow);
   }
-  // sel: bytes (2 kb, 2 kb + 1) of a dword pair into the high half
-  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t sel) const {
+  // s2/b2: the scales/biases of groups kb (low half) and 4 + kb (high half)
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t s2, uint32_t b2) const {
     const int h = st >> 2, i = st & 3;
-    const float sc = __uint_as_float(__builtin_amdgcn_perm(h ? sv.w : sv.y, h ? sv.z : sv.x, sel));
-    const float bi = __uint_as_float(__builtin_amdgcn_perm(h ? bv.w : bv.y, h ? bv.z : bv.x, sel));
+    const float sc = __uint_as_float(h ? s2 & 0xffff0000u : s2 << 16);
+    const float bi = __uint_as_float(h ? b2 & 0xffff0000u : b2 << 16);
     const Dequant dq(sc, bi);
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
     uint32_t r[4];
@@ -169,7 +174,7 @@ struct BChunk<true, true> {
       b[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.b) + mrow + g * 2u);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t, uint32_t) const {
     const int h = st >> 2, i = st & 3;
     const Dequant dq(bf16_to_f32(s[h]), bf16_to_f32(b[h]));
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
@@ -193,7 +198,7 @@ struct BChunk<false, TAIL> {
       for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 16 * i);
     }
   }
-  __device__ __forceinline__ bf16x8_t step(int st, uint32_t, uint32_t) const {
+  __device__ __forceinline__ bf16x8_t step(int st, uint32_t, uint32_t, uint32_t) const {
     uint32_t r[4];
     permute_word(v[st >> 2][st & 3], r);
     return as_operand(r);
@@ -237,7 +242,31 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     a_u[j] = u;
     a_off[j] = r * kRowBytes + u * 16;
   }
-  uint4 ar[kItems];
+  // scale staging (Q4, full chunks): vector v = tid + j * threads -> (proj,
+  // scales or biases, column of the block); 16 bytes = the chunk's 8 groups
+  constexpr int kCols = WAVES * NBW * 16;
+  constexpr bool kLdsScales = Q4 && !TAIL;
+  constexpr int kSVecs = kLdsScales ? PROJ * 2 * kCols : 0;
+  constexpr int kSItems = (kSVecs + kThreads - 1) / kThreads;
+  constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
+  const uint16_t* sv_src[kSItems > 0 ? kSItems : 1];
+#pragma unroll
+  for (int j = 0; j < kSItems; ++j) {
+    static_assert(kCols % 64 == 0, "a wave's vectors share one (projection, scales or biases)");
+    const uint32_t v = min(tid + j * kThreads, static_cast<uint32_t>(kSVecs - 1));
+    // (projection, scales or biases) is wave-uniform: select it in SGPRs (an
+    // indexed private array of pointers would go to scratch)
+    const uint32_t q = __builtin_amdgcn_readfirstlane(v / kCols);
+    const uint32_t col = min(slice * kCols + v % kCols, N - 1);
+    const uint16_t *ps0 = w[0].s, *pb0 = w[0].b, *ps1 = w[PROJ - 1].s, *pb1 = w[PROJ - 1].b;
+    VM_KEEP(ps0);  // opaque copies: a select of loads from `w` would become an indexed load
+    VM_KEEP(pb0);
+    VM_KEEP(ps1);
+    VM_KEEP(pb1);
+    const uint16_t* base = q >= 2 ? ((q & 1u) ? pb1 : ps1) : ((q & 1u) ? pb0 : ps0);
+    sv_src[j] = base + static_cast<size_t>(col) * G;
+  }
+  uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1];
   auto a_load = [&](uint32_t g0, bool tail) {
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
@@ -246,22 +275,30 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       if (tail && g0 + a_u[j] / 4 >= G) src = reinterpret_cast<const uint16_t*>(g_zero_page);
       ar[j] = ldg16(src);
     }
+#pragma unroll
+    for (int j = 0; j < kSItems; ++j) sr[j] = ldg16(sv_src[j] + g0);
+  };
+  // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
+  auto pair_perm = [](const uint4 v) {
+    return make_uint4((v.x & 0xffffu) | (v.z << 16), (v.x >> 16) | (v.z & 0xffff0000u),
+                      (v.y & 0xffffu) | (v.w << 16), (v.y >> 16) | (v.w & 0xffff0000u));
   };
   auto a_store = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
       if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
-      const uint32_t a = ar[j].x, b = ar[j].y, c = ar[j].z, d = ar[j].w;
-      *reinterpret_cast<uint4*>(s_a0 + buf * kStageBytes + a_off[j]) =
-          make_uint4((a & 0xffffu) | (c << 16), (a >> 16) | (c & 0xffff0000u),  // (x0, x4) (x1, x5)
-                     (b & 0xffffu) | (d << 16), (b >> 16) | (d & 0xffff0000u));  // (x2, x6) (x3, x7)
+      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + a_off[j]) = pair_perm(ar[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < kSItems; ++j) {
+      if (kSVecs % kThreads != 0 && tid + j * kThreads >= static_cast<uint32_t>(kSVecs)) continue;
+      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + kStageBytes + (tid + j * kThreads) * 16) = pair_perm(sr[j]);
     }
   };
 
   // B: lane -> (column lane%16 of each block, group g0 + lane/16); columns
   // past N read the last row and are not stored
   const uint32_t bn = lane & 15u, bkb = lane >> 4;
-  const uint32_t sel = 0x0c0cu | ((2u * bkb) << 16) | ((2u * bkb + 1u) << 24);
   uint32_t wrow[NBW], mrow[NBW];
 #pragma unroll
   for (int nb = 0; nb < NBW; ++nb) {
@@ -294,7 +331,20 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   const uint32_t am = lane & 15u, akb = lane >> 4;
   const uint32_t a_lane = am * kRowBytes + akb * 64;
   auto compute = [&](int buf, const BChunk<Q4, TAIL> (&bc)[PROJ][NBW]) {
-    const uint8_t* s_a = s_a0 + buf * kStageBytes + a_lane;
+    const uint8_t* s_a = s_a0 + buf * kStage + a_lane;
+    uint32_t s2[PROJ][NBW], b2[PROJ][NBW];
+#pragma unroll
+    for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+      for (int nb = 0; nb < NBW; ++nb) {
+        s2[pj][nb] = b2[pj][nb] = 0;
+        if constexpr (kLdsScales) {
+          const uint32_t col = wave * NBW * 16 + nb * 16 + bn;
+          const uint32_t* sv = reinterpret_cast<const uint32_t*>(s_a0 + buf * kStage + kStageBytes);
+          s2[pj][nb] = sv[((pj * 2 + 0) * kCols + col) * 4 + bkb];
+          b2[pj][nb] = sv[((pj * 2 + 1) * kCols + col) * 4 + bkb];
+        }
+      }
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
       bf16x8_t aop[MBU];
@@ -306,7 +356,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-          const bf16x8_t bop = bc[pj][nb].step(st, magic, sel);
+          const bf16x8_t bop = bc[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb]);
 #pragma unroll
           for (int mb = 0; mb < MBU; ++mb)
             acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
@@ -379,7 +429,7 @@ __global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(VM_G
 void k_grouped(GroupedLaunch p) {
   static_assert(kBM % 16 == 0 && kBM <= 64, "tiles are one to four 16-row blocks");
   constexpr bool Q4 = EPI != kEpiLogits;
-  extern __shared__ uint4 s_dyn[];  // two A stages of kStageBytes
+  extern __shared__ uint4 s_dyn[];  // two stages of stage_bytes<...>()
   uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
   const uint32_t tid = threadIdx.x;
 
@@ -633,7 +683,7 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
 
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
-  constexpr uint32_t lds = 2 * kStageBytes;
+  constexpr uint32_t lds = 2 * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
   auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL>;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
