@@ -12,11 +12,12 @@
 //            features).  Workgroups are dealt to the eight XCDs round-robin;
 //            the slices of one row tile take blocks of the same XCD so that
 //            they share its L2 copy of the tile's A rows.  K runs in chunks of
-//            eight 32-input groups: the A rows are staged in LDS (double
-//            buffered, 32 lanes per 512-byte row segment, pair-permuted to
-//            match the dequantised weights), each lane dequantises one
-//            16-byte Q4 group per chunk and projection into bf16 (f16 magic
-//            number + v_fma_mix + v_cvt_pk_bf16_f32) and feeds
+//            eight 32-input groups.  Per chunk the block stages in LDS (double
+//            buffered): the A rows (32 lanes per 512-byte row segment,
+//            pair-permuted to match the dequantised weights), the Q4 weight
+//            row chunks (8 lanes per 128-byte line) and the scale and bias
+//            vectors.  Each lane dequantises its 16-byte Q4 groups into bf16
+//            (f16 magic number + v_fma_mix + v_cvt_pk_bf16_f32) and feeds
 //            v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The MFMA loop
 //            is specialised on the number of 16-row blocks in use, so it has
 //            no branch.  Epilogues: SwiGLU of gate and up, bf16 rows (down),
@@ -54,9 +55,22 @@ constexpr int kStageBytes = kBM * kRowBytes;
 // Bytes of one LDS stage of a grouped GEMM instance: the A rows, then for Q4
 // weights without a tail chunk the chunk's scale and bias vectors of every
 // column of the block (16 bytes each).
+#ifndef VM_LDS_B
+#define VM_LDS_B 1
+#endif
+constexpr int kWColBytes = kCG * 16 + 16;  // LDS bytes per staged weight row chunk (+16 against bank conflicts)
+
+// Q4 weights staged through LDS (coalesced 128-byte row loads by the whole
+// block) rather than loaded by the MFMA lanes themselves.
+template <int EPI, bool TAIL>
+constexpr bool lds_weights() {
+  return VM_LDS_B && EPI != kEpiLogits && !TAIL;
+}
+
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 constexpr int stage_bytes() {
-  return kStageBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0);
+  return kStageBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
+         (lds_weights<EPI, TAIL>() ? PROJ * WAVES * NBW * 16 * kWColBytes : 0);
 }
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -266,7 +280,27 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     const uint16_t* base = q >= 2 ? ((q & 1u) ? pb1 : ps1) : ((q & 1u) ? pb0 : ps0);
     sv_src[j] = base + static_cast<size_t>(col) * G;
   }
-  uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1];
+  // weight staging (lds_weights): item it = tid + j * threads -> (projection,
+  // column of the block, group of the chunk); eight lanes read one row's
+  // 128-byte chunk line.  The projection is the same for all items of one j.
+  constexpr bool kLdsB = lds_weights<EPI, TAIL>();
+  constexpr int kWVecs = kLdsB ? PROJ * kCols * kCG : 0;
+  constexpr int kWItems = kWVecs / kThreads;
+  constexpr int kWArea = kStageBytes + (kLdsScales ? PROJ * 2 * kCols * 16 : 0);
+  static_assert(!kLdsB || (kWVecs % kThreads == 0 && (kCols * kCG) % kThreads == 0), "whole items per thread");
+  const uint8_t* w_src[kWItems > 0 ? kWItems : 1];
+  uint32_t w_off[kWItems > 0 ? kWItems : 1];
+#pragma unroll
+  for (int j = 0; j < kWItems; ++j) {
+    constexpr int kPerProj = kCols * kCG;
+    const uint32_t it = tid + j * kThreads;
+    const int pj = (j * kThreads) / kPerProj;  // compile-time
+    const uint32_t ci = (it % kPerProj) / kCG, g = it % kCG;
+    const uint32_t col = min(slice * kCols + ci, N - 1);
+    w_src[j] = reinterpret_cast<const uint8_t*>(w[pj].w) + static_cast<size_t>(col) * (K / 2) + g * 16u;
+    w_off[j] = kWArea + (pj * kCols + ci) * kWColBytes + g * 16u;
+  }
+  uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1], wr[kWItems > 0 ? kWItems : 1];
   auto a_load = [&](uint32_t g0, bool tail) {
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
@@ -277,6 +311,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     }
 #pragma unroll
     for (int j = 0; j < kSItems; ++j) sr[j] = ldg16(sv_src[j] + g0);
+#pragma unroll
+    for (int j = 0; j < kWItems; ++j) wr[j] = ldg16(w_src[j] + g0 * 16u);
   };
   // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
   auto pair_perm = [](const uint4 v) {
@@ -294,6 +330,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       if (kSVecs % kThreads != 0 && tid + j * kThreads >= static_cast<uint32_t>(kSVecs)) continue;
       *reinterpret_cast<uint4*>(s_a0 + buf * kStage + kStageBytes + (tid + j * kThreads) * 16) = pair_perm(sr[j]);
     }
+#pragma unroll
+    for (int j = 0; j < kWItems; ++j) *reinterpret_cast<uint4*>(s_a0 + buf * kStage + w_off[j]) = wr[j];
   };
 
   // B: lane -> (column lane%16 of each block, group g0 + lane/16); columns
@@ -332,6 +370,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   const uint32_t a_lane = am * kRowBytes + akb * 64;
   auto compute = [&](int buf, const BChunk<Q4, TAIL> (&bc)[PROJ][NBW]) {
     const uint8_t* s_a = s_a0 + buf * kStage + a_lane;
+    BChunk<Q4, TAIL> bl[PROJ][NBW];
     uint32_t s2[PROJ][NBW], b2[PROJ][NBW];
 #pragma unroll
     for (int pj = 0; pj < PROJ; ++pj)
@@ -352,11 +391,24 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       for (int mb = 0; mb < MBU; ++mb)
         aop[mb] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
                                                    s_a + mb * 16 * kRowBytes + (st >> 2) * 256 + (st & 3) * 16));
+      if constexpr (kLdsB) {
+        if ((st & 3) == 0) {  // the lane's group 4 h + kb of each of its rows, from LDS
+#pragma unroll
+          for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+            for (int nb = 0; nb < NBW; ++nb) {
+              const uint32_t col = wave * NBW * 16 + nb * 16 + bn;
+              bl[pj][nb].w[st >> 2] = *reinterpret_cast<const uint4*>(
+                  s_a0 + buf * kStage + kWArea + (pj * kCols + col) * kWColBytes + ((st >> 2) * 4 + bkb) * 16);
+            }
+        }
+      }
 #pragma unroll
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-          const bf16x8_t bop = bc[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb]);
+          const bf16x8_t bop = kLdsB ? bl[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb])
+                                     : bc[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb]);
 #pragma unroll
           for (int mb = 0; mb < MBU; ++mb)
             acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
@@ -369,7 +421,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   // makes the end of a chunk wait for them; an unrolled ping-pong without
   // that wait, and a third register set, both measured slower here.
   a_load(0, tail_chunk(0));
-  b_load(b0, 0, tail_chunk(0));
+  if constexpr (!kLdsB) b_load(b0, 0, tail_chunk(0));
   a_store(0);
   __syncthreads();
   for (uint32_t c = 0; c < chunks; ++c) {
@@ -377,15 +429,17 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     const bool more = c + 1 < chunks;
     if (more) {
       a_load((c + 1) * kCG, tail_chunk(c + 1));
-      b_load(b1, (c + 1) * kCG, tail_chunk(c + 1));
+      if constexpr (!kLdsB) b_load(b1, (c + 1) * kCG, tail_chunk(c + 1));
     }
     compute(buf, b0);
     if (more) {
       a_store(buf ^ 1);
+      if constexpr (!kLdsB) {
 #pragma unroll
-      for (int pj = 0; pj < PROJ; ++pj)
+        for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
-        for (int nb = 0; nb < NBW; ++nb) b0[pj][nb] = b1[pj][nb];
+          for (int nb = 0; nb < NBW; ++nb) b0[pj][nb] = b1[pj][nb];
+      }
     }
     __syncthreads();
   }
@@ -714,13 +768,13 @@ uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups) { return (rows + kBM 
 
 // block shapes (waves, 16-column blocks per wave) of the gate/up and down GEMMs
 #ifndef VM_GU_WAVES
-#define VM_GU_WAVES 4
+#define VM_GU_WAVES 8
 #endif
 #ifndef VM_GU_NBW
 #define VM_GU_NBW 1
 #endif
 #ifndef VM_DN_WAVES
-#define VM_DN_WAVES 4
+#define VM_DN_WAVES 8
 #endif
 #ifndef VM_DN_NBW
 #define VM_DN_NBW 2
