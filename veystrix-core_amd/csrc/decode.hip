@@ -6,10 +6,10 @@
 //
 //   k_front   router logits x . Wr^T (one row per wave, bf16 dot2) and the
 //             shared expert's H -> 1 Q4 gate with its sigmoid.
-//   k_gateup  in every block of a routed pair, wave 0 recomputes the token's
-//             softmax from the logits and finds the expert of its slot's rank
-//             (ballot search + candidate ranking, no sort), maps it to its slot and
-//             hands the route word to the other waves through one barrier.
+//   k_gateup  in every block of a routed pair, every wave recomputes the
+//             token's softmax from the logits and finds the expert of its
+//             slot's rank (ballot search + candidate ranking, no sort) and maps
+//             it to its slot: no barrier stands before the weight loads.
 //             Every lane then streams gate and up Q4/G32 rows against its
 //             activation groups held in registers; SwiGLU runs on the lanes
 //             that hold the row sums.  Shared-expert pairs skip the selection.
@@ -555,12 +555,14 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RPW = RPI * U;
   constexpr int RPB = RPW * kGuWaves;
-  __shared__ uint32_t s_word;
-  __shared__ typename Cand<A>::T s_cand[kMaxCand];
+  // every wave runs the selection itself (its own candidate list), so no
+  // barrier stands between the selection and the weight loads
+  __shared__ typename Cand<A>::T s_cands[kGuWaves][kMaxCand];
 
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
+  typename Cand<A>::T* s_cand = s_cands[wave];
   const uint32_t lr = lane % LPR;
   const uint32_t rw = lane / LPR;
   const uint32_t pair = blockIdx.y;
@@ -589,7 +591,7 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
   //    lane's activation groups
   float lg[kMaxExpertsPerLane];
   int32_t tab[kMaxExpertsPerLane];
-  if (select && wave == 0) {
+  if (select) {
     load_logits(p.logits + static_cast<size_t>(t) * E, E, lane, lg);
     if (p.slot_table != nullptr) {
 #pragma unroll
@@ -609,24 +611,19 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
   GateKeys<A> keys;
   uint32_t word = 0;
   if (select) {
-    if (wave == 0) {
-      softmax_keys<A>(lg, E, lane, keys);
-      if (p.trace != nullptr) tr.mark(5);
-      const uint32_t e = select_rank<A>(keys, p.slots, j, lane, s_cand);
-      uint32_t w = e;
-      if (p.slot_table != nullptr) {
-        const uint32_t m_e = e >> 6, l_e = e & 63u;
-        int32_t slot = -1;
+    softmax_keys<A>(lg, E, lane, keys);
+    if (p.trace != nullptr) tr.mark(5);
+    const uint32_t e = select_rank<A>(keys, p.slots, j, lane, s_cand);
+    word = e;
+    if (p.slot_table != nullptr) {
+      const uint32_t m_e = e >> 6, l_e = e & 63u;
+      int32_t slot = -1;
 #pragma unroll
-        for (int m = 0; m < kMaxExpertsPerLane; ++m)
-          if (m == static_cast<int>(m_e)) slot = __builtin_amdgcn_readlane(tab[m], l_e);
-        w = route_word(slot);
-      }
-      if (lane == 0) s_word = w;
-      if (p.trace != nullptr) tr.mark(6);
+      for (int m = 0; m < kMaxExpertsPerLane; ++m)
+        if (m == static_cast<int>(m_e)) slot = __builtin_amdgcn_readlane(tab[m], l_e);
+      word = route_word(slot);
     }
-    __syncthreads();
-    word = s_word;
+    if (p.trace != nullptr) tr.mark(6);
   } else if (!shared_pair) {
     word = p.routes[t * p.slots + j];
   }
