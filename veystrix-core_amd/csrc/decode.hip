@@ -16,7 +16,7 @@
 //             One block per token publishes the ordered selection (indices,
 //             scores, route words) for k_down.
 //   k_down    down Q4/G32 GEMV of every slot of a token for a tile of output
-//             rows (wave w owns slots w, w+4, w+8), then the router-score
+//             rows (one slot per wave), then the router-score
 //             combine with the shared term after one barrier.
 //   k_select  softmax + top-k alone (router entry point, split layer path).
 //
@@ -728,7 +728,7 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
 
 constexpr int kDownMaxSlots = 12;                         // MAX_TOP_K (10) + shared, rounded up
 #ifndef VM_DOWN_WAVES
-#define VM_DOWN_WAVES 8
+#define VM_DOWN_WAVES 12
 #endif
 constexpr int kDownWaves = VM_DOWN_WAVES;                  // waves per down block
 constexpr int kDownBlock = kDownWaves * 64;
