@@ -234,13 +234,18 @@ def run_grouped(name, tokens, layers, reps, seed):
     return result
 
 
-def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_000_000_000, bias_scale=1.0):
+def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_000_000_000, bias_scale=1.0,
+              device_lru=False):
     """The 48-layer stack at batch 1 with an LRU expert pool of `pool_bytes`
-    (3,051 slots at 6 GB, the reference's sizing) and Zipf(1.1) routing; misses
-    are staged from pinned host records with hipMemcpyAsync on a side stream.
-    The host store holds `store_records` distinct records aliased over the
-    24,576 (layer, expert) ids (the bytes moved per miss are the same).
-    `bias_scale` multiplies the log-Zipf logit bias (1 = the stated recipe)."""
+    (3,051 slots at 6 GB, the reference's sizing) and Zipf(1.1) routing.
+    Host LRU (default): every layer syncs its routes to the host, which assigns
+    slots and stages the misses from pinned host records with hipMemcpyAsync
+    on a side stream.  `device_lru`: the LRU state lives on the GPU and the
+    misses are read by a kernel straight from the pinned records, so no layer
+    waits for the host.  The host store holds `store_records` distinct records
+    aliased over the 24,576 (layer, expert) ids (the bytes moved per miss are
+    the same).  `bias_scale` multiplies the log-Zipf logit bias (1 = the
+    stated recipe)."""
     import torch
 
     from veymoe import assemble, synth
@@ -283,22 +288,28 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
                                shared_expert_gate=q4(1, spec.hidden)))
     x = torch.randn((warm_tokens + tokens, spec.layers, spec.hidden), device=device, generator=gen)
     x = x.to(torch.bfloat16)
+    lru = pool.attach_device_lru(store) if device_lru else None
+
+    def counts():
+        if lru is not None:
+            c = lru.stats()
+            return c["routed_hits"], c["misses"], c["misses"] * layout.record_bytes
+        return (sum(m.switch_mlp.hits for m in layers), sum(m.switch_mlp.misses for m in layers),
+                pool.bytes_staged)
+
     for t in range(warm_tokens):
         for layer in range(spec.layers):
             layers[layer](x[t, layer:layer + 1])
     torch.cuda.synchronize()
-    hits0 = sum(m.switch_mlp.hits for m in layers)
-    misses0 = sum(m.switch_mlp.misses for m in layers)
-    staged0 = pool.bytes_staged
+    hits0, misses0, staged0 = counts()
     start = time.perf_counter()
     for t in range(warm_tokens, warm_tokens + tokens):
         for layer in range(spec.layers):
             layers[layer](x[t, layer:layer + 1])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - start
-    hits = sum(m.switch_mlp.hits for m in layers) - hits0
-    misses = sum(m.switch_mlp.misses for m in layers) - misses0
-    staged = pool.bytes_staged - staged0
+    hits1, misses1, staged1 = counts()
+    hits, misses, staged = hits1 - hits0, misses1 - misses0, staged1 - staged0
     # pinned host -> HBM copy rate of one large transfer, the bound of the miss path
     big = store.buffer[: min(store_records, 512)]
     dst = torch.empty(big.shape, dtype=torch.uint8, device=device)
@@ -307,7 +318,8 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
     dst.copy_(big, non_blocking=True)
     torch.cuda.synchronize()
     h2d = big.numel() / (time.perf_counter() - t0) / 1e9
-    result = {"tokens": tokens, "layers": spec.layers, "bias_scale": bias_scale,
+    result = {"lru": "device" if device_lru else "host", "tokens": tokens, "layers": spec.layers,
+              "bias_scale": bias_scale,
               "tok_s": round(tokens / elapsed, 2),
               "ms_per_token": round(elapsed * 1e3 / tokens, 3), "pool_slots": pool.slots,
               "hit_rate": round(hits / max(1, hits + misses), 4), "misses_per_token": round(misses / tokens, 1),
@@ -453,7 +465,9 @@ def main():
         log("48-layer stack, LRU pool of 6 GB, misses from pinned host")
         # the stated Zipf(1.1) recipe, and its logit bias scaled to reach the ~60% hit rate
         result["stack48_lru"] = {"zipf_recipe": run_stack(args.seed),
-                                 "hit_rate_60": run_stack(args.seed, bias_scale=0.45)}
+                                 "hit_rate_60": run_stack(args.seed, bias_scale=0.45),
+                                 "device_lru_zipf_recipe": run_stack(args.seed, device_lru=True),
+                                 "device_lru_hit_rate_60": run_stack(args.seed, bias_scale=0.45, device_lru=True)}
     if args.copy_probe_mib:
         n = args.copy_probe_mib * (1 << 20) // 2
         probe_in = torch.ones(n, dtype=torch.bfloat16, device=device)

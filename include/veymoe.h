@@ -24,6 +24,9 @@
  *   vm_moe_grouped     _one_pass/_issue gather_qmm path models/flashnext/expert_cache.py:1949-2037 (rows > 8)
  *   vm_weighted_combine weighted_combine                models/flashnext/metal_runtime.py:145-191
  *   vm_pool_stage      ExpertPool.fill/_fill_part       models/flashnext/expert_pool.py:201-220,258-287
+ *   vm_moe_layer_lru   _pool_pass (route sync, assign, fill, execute)
+ *                                                       models/flashnext/expert_cache.py:1709-1772,1842-1947
+ *                                                       models/flashnext/expert_pool.py:123-159,201-220
  *   vm_available       flashnext_native_available       metal_runtime_native.mm:196-201
  *   vm_last_error      flashnext_native_get_last_error  metal_runtime_native.mm:203-209
  */
@@ -197,6 +200,58 @@ typedef struct VmLayerArgs {
 #define VM_PHASE_ROUTER 1u
 #define VM_PHASE_EXPERTS 2u
 
+/* vm_moe_layer_lru: the decode layer (tokens <= VM_LAYER_MAX_TOKENS) over an
+ * expert pool whose LRU state lives on the device, so the call never waits for
+ * the host.  It replaces the reference's per-layer route sync + host
+ * ExpertPool.assign + fill (expert_cache.py:1738-1749, 1842-1947;
+ * expert_pool.py:123-159, 201-220): the router selects on the device, one
+ * block applies assign() to the routed ids of the call, missed records are
+ * copied by a kernel straight from pinned host memory into their new slots,
+ * then the experts run through the updated slot table.
+ *
+ * assign() semantics, exactly as the reference's LRU: the distinct experts of
+ * the call in first-seen order (tokens in order, slots in rank order); hits
+ * move to the most recent end in that order; then each miss, in that order,
+ * takes the next victim: free slots first (in the order the reference's free
+ * list pops them), then the least recently used key, whose table entry is
+ * cleared.  Recency is a per-slot stamp: every slot carries a distinct stamp,
+ * free slots the smallest, and the victims of a call are the slots with the
+ * smallest stamps that are not hits of that call.
+ *
+ * State (device memory owned by the caller, updated in place):
+ *   slot_table  [layers, expert_count] int32: expert -> slot, -1 = absent
+ *               (row `layer` replaces VmLayerArgs.slot_table, which is ignored)
+ *   slot_owner  [slots] int32: layer * expert_count + expert, -1 = free
+ *   slot_stamp  [slots] uint64, all distinct and nonzero
+ *   counters    [4 + 4 * layers] uint64: last stamp issued, distinct hits,
+ *               distinct misses, routed hits (routed positions minus distinct
+ *               misses, the reference's StreamingSwitchGLU.hits); then per
+ *               layer: distinct hits, distinct misses, routed hits, routed ids
+ *   host_row    [layers, expert_count] int32: row of the expert's record in
+ *               host_store (-1: no record)
+ *   host_store  pinned host memory (hipHostMalloc), host_records rows of
+ *               host_stride bytes; rows are read by the GPU over the host link
+ * slots must equal VmLayerArgs.pool.records and be at least tokens * top_k.
+ * A miss whose expert has no host record is left unfilled and sets status bit
+ * 4; a routed id outside 0..expert_count-1 is skipped and sets status bit 8;
+ * a state with fewer candidate slots than misses (stamps not distinct or
+ * zero) maps only the misses it can and sets status bit 16.  Calls that
+ * overlap on one state race: issue them on one stream. */
+typedef struct VmDeviceLru {
+  int32_t* slot_table;
+  int32_t* slot_owner;
+  uint64_t* slot_stamp;
+  uint64_t* counters;
+  const int32_t* host_row;
+  const void* host_store;
+  uint64_t host_stride;
+  uint64_t host_records;
+  uint32_t layers;
+  uint32_t layer;
+  uint32_t slots;
+  uint32_t reserved;
+} VmDeviceLru;
+
 /* vm_moe_grouped: the expert block of the grouped path for any token count
  * with given routes (SwitchGLU over expert ids, expert_cache.py:1949-2037):
  * token-by-expert sort on the device, MFMA grouped gate/up/SwiGLU and down
@@ -239,6 +294,8 @@ int vm_router_topk(const VmRouterArgs* args, void* stream);
 uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
                                 uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype);
 int vm_moe_layer(const VmLayerArgs* args, void* stream);
+/* Workspace: vm_moe_layer_workspace() of the same shape. */
+int vm_moe_layer_lru(const VmLayerArgs* args, const VmDeviceLru* lru, void* stream);
 
 uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size,
                                   uint32_t inter_size, uint32_t expert_count, uint32_t act_dtype);

@@ -33,6 +33,7 @@ def test_struct_layouts_match_the_header(tmp_path):
     structs = {
         "VmQ4Proj": _lib.VmQ4Proj, "VmPoolView": _lib.VmPoolView, "VmMoeArgs": _lib.VmMoeArgs,
         "VmRouterArgs": _lib.VmRouterArgs, "VmLayerArgs": _lib.VmLayerArgs, "VmGroupedArgs": _lib.VmGroupedArgs,
+        "VmDeviceLru": _lib.VmDeviceLru,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for name, cls in structs.items():
@@ -100,6 +101,34 @@ def test_router_and_layer_bounds():
     layer.tokens, layer.hidden_size, layer.expert_count, layer.top_k = 9, 64, 8, 2
     layer.inter_size, layer.group_size = 64, 32
     assert lib.vm_moe_layer(ctypes.byref(layer), None) == _lib.VM_EINVAL
+
+
+def _lru_call(**kw):
+    """vm_moe_layer_lru on fake pointers: every case must fail validation."""
+    a = _lib.VmLayerArgs()
+    a.x, a.output, a.router_weight = 256, 512, 768
+    a.tokens, a.hidden_size, a.inter_size, a.expert_count, a.top_k, a.group_size = 1, 64, 64, 8, 2, 32
+    a.pool.base, a.pool.record_stride, a.pool.records = 4096, 4096, 16
+    lru = _lib.VmDeviceLru()
+    lru.slot_table, lru.slot_owner, lru.slot_stamp, lru.counters, lru.host_row = 1024, 1056, 1088, 1120, 1152
+    lru.host_store, lru.host_stride, lru.host_records = 8192, 4096, 8
+    lru.layers, lru.layer, lru.slots = 2, 0, 16
+    for k, v in kw.items():
+        target = lru if hasattr(lru, k) and k not in ("slot_table",) and not hasattr(a, k) else a
+        setattr(target, k, v)
+    return _lib.lib().vm_moe_layer_lru(ctypes.byref(a), ctypes.byref(lru), None)
+
+
+@pytest.mark.parametrize("field,value,code,message", [
+    ("tokens", 9, _lib.VM_EUNSUPPORTED, "decode calls"),
+    ("phases", 1, _lib.VM_EINVAL, "phases"),
+    ("host_store", None, _lib.VM_EINVAL, "state pointers"),
+    ("layer", 2, _lib.VM_EINVAL, "outside"),
+    ("slots", 15, _lib.VM_EINVAL, "must equal the pool records"),
+])
+def test_layer_lru_rejects_bad_arguments_without_a_device(field, value, code, message):
+    assert _lru_call(**{field: value}) == code
+    assert message in _lib.last_error()
 
 
 def test_pool_stage_checks_indices_before_copying():

@@ -340,9 +340,10 @@ int vm_router_topk(const VmRouterArgs* a, void* stream_ptr) {
 
 // -------------------------------------------------------------- layer ---
 // workspace: [reserved] [logits T*E f32] [act T*S*I] [sig T] [inds T*K] [scores T*K] [words T*K]
+//            [fill list of the device LRU: count, source rows, slots]
 
 struct LayerWs {
-  uint64_t logits, act, sig, inds, scores, words, total;
+  uint64_t logits, act, sig, inds, scores, words, fill, total;
 };
 
 static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_t E, uint32_t dtype) {
@@ -354,7 +355,8 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   w.inds = w.sig + align_up(uint64_t(T) * act_bytes(dtype));
   w.scores = w.inds + align_up(uint64_t(T) * K * 4);
   w.words = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
-  w.total = w.words + align_up(uint64_t(T) * K * 4);
+  w.fill = w.words + align_up(uint64_t(T) * K * 4);
+  w.total = w.fill + align_up(4 + 8 * uint64_t(vm::kLruMaxRouted));
   return w;
 }
 
@@ -407,11 +409,10 @@ uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden
 static int layer_decode(const VmLayerArgs* a, hipStream_t stream);
 static int layer_grouped(const VmLayerArgs* a, hipStream_t stream);
 
-int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
+static int validate_layer(const VmLayerArgs* a) {
   if (a == nullptr) return fail(VM_EINVAL, "null arguments");
-  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
-  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size;
-  int rc = validate_router(T, H, a->expert_count, K, a->act_dtype);
+  const uint32_t H = a->hidden_size, I = a->inter_size;
+  int rc = validate_router(a->tokens, H, a->expert_count, a->top_k, a->act_dtype);
   if (rc != VM_OK) return rc;
   if (a->group_size != 32) return fail(VM_EUNSUPPORTED, "group_size must be 32");
   if (I == 0 || I % 32) return fail(VM_EINVAL, "Q4/G32 projection inputs must be group aligned");
@@ -437,6 +438,14 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   if (rc != VM_OK) return rc;
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  return VM_OK;
+}
+
+int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
+  int rc = validate_layer(a);
+  if (rc != VM_OK) return rc;
+  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size;
   if (use_grouped(T, a->act_dtype)) return layer_grouped(a, stream);
   if (T <= VM_LAYER_MAX_TOKENS) return layer_decode(a, stream);
   // fp32 activations above the decode bound: decode kernels in chunks of
@@ -556,6 +565,112 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   e = vm::launch_down(d, stream);
   if (e != hipSuccess) return hip_fail(e, "down launch");
   return VM_OK;
+}
+
+// End of the last record part: the bytes of a record a fill copies.
+static uint64_t record_end(const VmPoolView& v, uint32_t hidden, uint32_t inter) {
+  const uint64_t w = uint64_t(inter) * hidden / 2, m = uint64_t(inter) * (hidden / 32) * 2;
+  const uint64_t dm = uint64_t(hidden) * (inter / 32) * 2;
+  const uint64_t sizes[VM_PARTS] = {w, m, m, w, m, m, w, dm, dm};
+  uint64_t end = 0;
+  for (int i = 0; i < VM_PARTS; ++i) end = v.part_offset[i] + sizes[i] > end ? v.part_offset[i] + sizes[i] : end;
+  return end;
+}
+
+// Device-accessible address of pinned host memory (cached for the last store).
+static int host_device_pointer(const void* host, const uint8_t** out) {
+  thread_local const void* last_host = nullptr;
+  thread_local const uint8_t* last_dev = nullptr;
+  if (host != last_host) {
+    void* dev = nullptr;
+    hipError_t e = hipHostGetDevicePointer(&dev, const_cast<void*>(host), 0);
+    if (e != hipSuccess || dev == nullptr)
+      return fail(VM_EINVAL, "host_store is not pinned host memory (hipHostGetDevicePointer: %s)",
+                  hipGetErrorString(e));
+    last_host = host;
+    last_dev = static_cast<const uint8_t*>(dev);
+  }
+  *out = last_dev;
+  return VM_OK;
+}
+
+int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_ptr) {
+  if (a == nullptr || lru == nullptr) return fail(VM_EINVAL, "null arguments");
+  const hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
+  if (T == 0 || T > VM_LAYER_MAX_TOKENS)
+    return fail(VM_EUNSUPPORTED, "the device LRU serves decode calls of 1..%d tokens", VM_LAYER_MAX_TOKENS);
+  if (a->phases != 0) return fail(VM_EINVAL, "vm_moe_layer_lru runs the whole layer (phases must be 0)");
+  if (lru->slot_table == nullptr || lru->slot_owner == nullptr || lru->slot_stamp == nullptr ||
+      lru->counters == nullptr || lru->host_row == nullptr || lru->host_store == nullptr)
+    return fail(VM_EINVAL, "device LRU state pointers are required");
+  if (a->pool.base == nullptr) return fail(VM_EINVAL, "the device LRU needs a pool view");
+  if (lru->layer >= lru->layers) return fail(VM_EINVAL, "layer %u is outside 0..%u", lru->layer, lru->layers);
+  if (lru->slots != a->pool.records)
+    return fail(VM_EINVAL, "LRU slots (%u) must equal the pool records (%u)", lru->slots, a->pool.records);
+  if (uint64_t(T) * K > lru->slots || uint64_t(T) * K > vm::kLruMaxRouted)
+    return fail(VM_EINVAL, "tokens * top_k = %u exceeds the pool or the %u routed ids of one call", T * K,
+                vm::kLruMaxRouted);
+  if (uint64_t(lru->layers) * E > 0x7fffffffull) return fail(VM_EINVAL, "layers * expert_count is too large");
+  VmLayerArgs r = *a;
+  r.slot_table = lru->slot_table + uint64_t(lru->layer) * E;
+  int rc = validate_layer(&r);
+  if (rc != VM_OK) return rc;
+  const uint64_t bytes = record_end(a->pool, H, I);
+  if (bytes % 16 || lru->host_stride % 16 || lru->host_stride < bytes || a->pool.header_size % 16)
+    return fail(VM_EINVAL, "records of %llu bytes need 16-byte aligned host rows of at least that size",
+                (unsigned long long)bytes);
+  if (!aligned16(lru->host_store)) return fail(VM_EINVAL, "host_store must be 16-byte aligned");
+  const uint8_t* host = nullptr;
+  rc = host_device_pointer(lru->host_store, &host);
+  if (rc != VM_OK) return rc;
+  const LayerWs w = layer_ws(T, K, I, a->shared_inter, E, a->act_dtype);
+  if (a->workspace == nullptr || a->workspace_bytes < w.total)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
+  char* ws = static_cast<char*>(a->workspace);
+
+  // 1. router logits, shared gate, softmax/top-k into inds/scores
+  r.phases = VM_PHASE_ROUTER;
+  rc = layer_decode(&r, stream);
+  if (rc != VM_OK) return rc;
+  // 2. assign() on the device state, 3. fill the misses from the host store
+  uint32_t* fill = reinterpret_cast<uint32_t*>(ws + w.fill);
+  vm::LruLaunch l{};
+  l.inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<const int32_t*>(ws + w.inds);
+  l.slot_table = lru->slot_table;
+  l.slot_owner = lru->slot_owner;
+  l.slot_stamp = lru->slot_stamp;
+  l.counters = lru->counters;
+  l.host_row = lru->host_row;
+  l.fill_count = fill;
+  l.fill_src = fill + 1;
+  l.fill_dst = fill + 1 + vm::kLruMaxRouted;
+  l.status = a->status;
+  l.host_records = lru->host_records;
+  l.routed = T * K;
+  l.experts = E;
+  l.layers = lru->layers;
+  l.layer = lru->layer;
+  l.slots = lru->slots;
+  hipError_t e = vm::launch_lru(l, stream);
+  if (e != hipSuccess) return hip_fail(e, "lru launch");
+  vm::FillLaunch f{};
+  f.count = l.fill_count;
+  f.src = l.fill_src;
+  f.dst = l.fill_dst;
+  f.host = host;
+  f.host_stride = lru->host_stride;
+  f.host_records = lru->host_records;
+  f.pool = const_cast<uint8_t*>(a->pool.base);
+  f.header = a->pool.header_size;
+  f.stride = a->pool.record_stride;
+  f.pool_records = a->pool.records;
+  f.record_bytes = bytes;
+  e = vm::launch_fill(f, stream);
+  if (e != hipSuccess) return hip_fail(e, "fill launch");
+  // 4. the experts through the updated slot table
+  r.phases = VM_PHASE_EXPERTS;
+  return layer_decode(&r, stream);
 }
 
 

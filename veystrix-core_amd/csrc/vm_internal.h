@@ -81,6 +81,40 @@ struct DownLaunch {
   int act_dtype;
 };
 
+// ------------------------------------------------------ device-side LRU --
+constexpr uint32_t kLruMaxRouted = 80;  // VM_LAYER_MAX_TOKENS * MAX_TOP_K
+constexpr uint32_t kNoRecord = 0xffffffffu;
+
+// assign() of one decode call on the device state (one block).
+struct LruLaunch {
+  const int32_t* inds;         // [routed] expert ids, tokens in order, slots in rank order
+  int32_t* slot_table;         // [layers, experts]
+  int32_t* slot_owner;         // [slots]
+  uint64_t* slot_stamp;        // [slots]
+  uint64_t* counters;          // [4 + 4 * layers]
+  const int32_t* host_row;     // [layers, experts]
+  uint32_t* fill_count;        // [1] misses of the call
+  uint32_t* fill_src;          // [routed] host row of miss m (kNoRecord: none)
+  uint32_t* fill_dst;          // [routed] slot of miss m
+  uint32_t* status;
+  uint64_t host_records;
+  uint32_t routed, experts, layers, layer, slots;
+};
+
+// Copy of the missed records from pinned host memory into their slots.
+struct FillLaunch {
+  const uint32_t* count;
+  const uint32_t* src;
+  const uint32_t* dst;
+  const uint8_t* host;         // device-accessible address of the pinned store
+  uint64_t host_stride, host_records;
+  uint8_t* pool;
+  uint64_t header, stride, pool_records, record_bytes;
+};
+
+hipError_t launch_lru(const LruLaunch& p, hipStream_t stream);
+hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
+
 // ---------------------------------------------------------- grouped path --
 #ifndef VM_GROUPED_ROWS
 #define VM_GROUPED_ROWS 64

@@ -113,6 +113,23 @@ VM_PHASE_ROUTER = 1
 VM_PHASE_EXPERTS = 2
 
 
+class VmDeviceLru(ctypes.Structure):
+    _fields_ = [
+        ("slot_table", _vp),
+        ("slot_owner", _vp),
+        ("slot_stamp", _vp),
+        ("counters", _vp),
+        ("host_row", _vp),
+        ("host_store", _vp),
+        ("host_stride", _c_u64),
+        ("host_records", _c_u64),
+        ("layers", _c_u32),
+        ("layer", _c_u32),
+        ("slots", _c_u32),
+        ("reserved", _c_u32),
+    ]
+
+
 class VmGroupedArgs(ctypes.Structure):
     _fields_ = [
         ("x", _vp),
@@ -143,6 +160,7 @@ SIGNATURES = {
     "vm_router_topk": (ctypes.c_int, [ctypes.POINTER(VmRouterArgs), _vp]),
     "vm_moe_layer_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_layer": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), _vp]),
+    "vm_moe_layer_lru": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), ctypes.POINTER(VmDeviceLru), _vp]),
     "vm_moe_grouped_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_grouped": (ctypes.c_int, [ctypes.POINTER(VmGroupedArgs), _vp]),
     "vm_weighted_combine": (ctypes.c_int, [_vp, _vp, _vp, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _vp]),

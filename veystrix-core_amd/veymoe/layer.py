@@ -267,6 +267,22 @@ class MoELayer:
         args.phases = 0
         lib = _lib.lib()
         sw = self.switch_mlp
+        lru = sw.pool.device_lru if sw.pool is not None else None
+        if lru is not None:
+            if tokens > MAX_DECODE_ROWS:
+                # the grouped path resolves its experts on the host: hand the
+                # LRU state back for this call
+                sw.pool.detach_device_lru()
+                try:
+                    return self.forward(flat)
+                finally:
+                    sw.pool.attach_device_lru(lru.store)
+            if tokens * self.top_k > lru.usable_slots:
+                raise ValueError("requested experts exceed expert pool capacity")
+            # router, assign, fill and experts on the device: no route sync
+            _lib.check(lib.vm_moe_layer_lru(args, lru.view(sw.layer_id), stream_handle()))
+            self.last_inds, self.last_scores = inds, scores
+            return out
         if sw.pool is not None and not sw._pool_fully_resident():
             # router, then the host LRU pass on synced routes, then the experts
             args.phases = _lib.VM_PHASE_ROUTER

@@ -17,7 +17,12 @@ Counterpart of the reference's ``ExpertPool`` (models/flashnext/expert_pool.py:7
   compute stream, and the copy stream first waits for the compute stream so a
   slot is overwritten only after its last reader (:19-22);
 * a failed fill invalidates its misses so no partial record becomes a hit
-  (``invalidate``, :222-231).
+  (``invalidate``, :222-231);
+* ``attach_device_lru`` moves the LRU state to the device (``DeviceLru``):
+  decode layers then assign, fill and run with ``vm_moe_layer_lru`` without
+  any route sync to the host (the reference syncs every layer,
+  expert_cache.py:1738-1749).  Recency there is one distinct stamp per slot,
+  converted from and back to this class's OrderedDict order exactly.
 """
 from __future__ import annotations
 
@@ -93,6 +98,7 @@ class ExpertPool:
         self._row_events = {}      # layer -> event after the last upload of its pinned row
         self._stage_events = None  # (compute reached the copies, copies done), reused
         self._stage_args = None    # ctypes index arrays, grown on demand
+        self.device_lru = None     # DeviceLru while the LRU state lives on the device
 
     @classmethod
     def from_bytes(cls, layout: RecordLayout, size_bytes: int, **kwargs):
@@ -115,8 +121,13 @@ class ExpertPool:
         self._host_table[layer, expert] = -1
         self._dirty.add(layer)
 
+    def _host_state(self, what: str) -> None:
+        if self.device_lru is not None:
+            raise RuntimeError(f"{what}: the LRU of this pool lives on the device (detach_device_lru first)")
+
     def assign(self, layer: int, experts: Iterable[int] | int):
         """Assign a distinct expert set that fits in the pool, or fail before mutation."""
+        self._host_state("assign")
         if isinstance(experts, (int, np.integer)):
             experts = [int(experts)]
         distinct = list(dict.fromkeys(int(e) for e in experts))
@@ -147,6 +158,7 @@ class ExpertPool:
 
     def invalidate(self, layer: int, misses) -> None:
         """Return the slots of failed fills to the free list, never as hits."""
+        self._host_state("invalidate")
         for expert, slot in misses:
             key = (layer, expert)
             if self._slot_of.get(key) == slot:
@@ -199,6 +211,7 @@ class ExpertPool:
     def place(self, layer: int, expert: int, slot: int) -> None:
         """Pin (layer, expert) to ``slot`` directly (resident setups); the slot
         must be free."""
+        self._host_state("place")
         key = (int(layer), int(expert))
         if key in self._slot_of:
             raise ValueError(f"{key} is already resident")
@@ -211,6 +224,7 @@ class ExpertPool:
 
     def place_all(self, layer: int, slots) -> None:
         """Pin expert e of ``layer`` to ``slots[e]`` for every e (resident setups)."""
+        self._host_state("place_all")
         slots = [int(s) for s in slots]
         taken = set(slots)
         if len(taken) != len(slots) or not taken.issubset(self._free):
@@ -239,6 +253,7 @@ class ExpertPool:
         Returns the completion event, which the next call records again."""
         if not misses:
             return None
+        self._host_state("stage")
         order = sorted(misses, key=lambda item: item[1])
         n = len(order)
         if self._stage_args is None or len(self._stage_args[0]) < n:
@@ -277,9 +292,133 @@ class ExpertPool:
             raise
 
 
+    # ------------------------------------------------------ device LRU ---
+    def attach_device_lru(self, source: HostRecordStore) -> "DeviceLru":
+        """Move the LRU state to the device; misses are then filled from
+        ``source`` by the GPU itself.  Host-side LRU calls raise until
+        ``detach_device_lru``."""
+        if self.device_lru is not None:
+            raise RuntimeError("a device LRU is already attached")
+        self.device_lru = DeviceLru(self, source)
+        return self.device_lru
+
+    def detach_device_lru(self) -> None:
+        """Bring the LRU state back from the device (one sync)."""
+        lru = self.device_lru
+        if lru is None:
+            return
+        table, owner, stamp = lru.state()
+        restore_from_stamps(self, owner, stamp)
+        if not np.array_equal(table, self._host_table):
+            raise RuntimeError("device slot table disagrees with the slot owners")
+        stats = lru.stats()
+        self.hits += stats["hits"]
+        self.misses += stats["misses"]
+        self.bytes_staged += stats["misses"] * self.layout.record_bytes
+        self.device_lru = None
+
+
+def stamp_state(pool: ExpertPool):
+    """The pool's LRU order as one distinct stamp per slot, the form the device
+    LRU keeps: free slots get 1..n in the order the free list pops them (from
+    its end), then resident keys n+1.. from least to most recently used.
+    Slots that are neither free nor resident keep stamp 0 (never chosen).
+    Returns (owner [slots] int32 = layer * experts + expert or -1,
+    stamp [slots] uint64, last stamp issued)."""
+    owner = np.full(pool.slots, -1, dtype=np.int32)
+    stamp = np.zeros(pool.slots, dtype=np.uint64)
+    free = pool._free
+    n = len(free)
+    for i, slot in enumerate(free):
+        stamp[slot] = n - i
+    for j, ((layer, expert), slot) in enumerate(pool._slot_of.items()):
+        owner[slot] = layer * pool.experts + expert
+        stamp[slot] = n + 1 + j
+    return owner, stamp, n + len(pool._slot_of)
+
+
+def restore_from_stamps(pool: ExpertPool, owner: np.ndarray, stamp: np.ndarray) -> None:
+    """Inverse of ``stamp_state``: rebuild the free list, the OrderedDict and
+    the host slot table of ``pool`` from per-slot owners and stamps."""
+    owner = np.asarray(owner)
+    stamp = np.asarray(stamp, dtype=np.uint64)
+    slots = np.arange(pool.slots)
+    free = slots[(owner < 0) & (stamp > 0)]
+    resident = slots[owner >= 0]
+    pool._free = [int(s) for s in free[np.argsort(stamp[free], kind="stable")[::-1]]]
+    pool._slot_of = OrderedDict()
+    pool._host_table[:] = -1
+    for slot in resident[np.argsort(stamp[resident], kind="stable")]:
+        layer, expert = divmod(int(owner[slot]), pool.experts)
+        pool._slot_of[(layer, expert)] = int(slot)
+        pool._host_table[layer, expert] = int(slot)
+    pool._dirty.clear()
+
+
+class DeviceLru:
+    """The LRU state of an ``ExpertPool`` on the device (``VmDeviceLru``):
+    the slot table (the pool's own device table), per-slot owners and stamps,
+    counters, and the host-store row of every (layer, expert)."""
+
+    def __init__(self, pool: ExpertPool, source: HostRecordStore):
+        if source.layout.record_bytes != pool.layout.record_bytes:
+            raise ValueError("host store records do not match the pool layout")
+        if not source.buffer.is_pinned():
+            raise ValueError("the host store must be pinned memory")
+        pool.sync_tables()
+        owner, stamp, last = stamp_state(pool)
+        dev = pool.device
+        self.pool = pool
+        self.store = source
+        self.usable_slots = pool.usable_slots
+        self.slot_owner = torch.from_numpy(owner).to(dev)
+        self.slot_stamp = torch.from_numpy(stamp.view(np.int64)).to(dev)
+        counters = np.zeros(4 + 4 * pool.layers, dtype=np.int64)
+        counters[0] = last
+        self.counters = torch.from_numpy(counters).to(dev)
+        host_row = np.full((pool.layers, pool.experts), -1, dtype=np.int32)
+        for (layer, expert), row in source._row_of.items():
+            if layer < pool.layers and expert < pool.experts:
+                host_row[layer, expert] = row
+        self.host_row = torch.from_numpy(host_row).to(dev)
+        self._views = {}
+
+    def view(self, layer: int) -> _lib.VmDeviceLru:
+        v = self._views.get(layer)
+        if v is None:
+            v = _lib.VmDeviceLru()
+            v.slot_table = self.pool.slot_table.data_ptr()
+            v.slot_owner = self.slot_owner.data_ptr()
+            v.slot_stamp = self.slot_stamp.data_ptr()
+            v.counters = self.counters.data_ptr()
+            v.host_row = self.host_row.data_ptr()
+            v.host_store = self.store.buffer.data_ptr()
+            v.host_stride = self.store.buffer.stride(0)
+            v.host_records = self.store.capacity
+            v.layers = self.pool.layers
+            v.layer = int(layer)
+            v.slots = self.pool.slots
+            self._views[layer] = v
+        return v
+
+    def stats(self, layer: int = None) -> dict:
+        """Counters (synchronizes): pool-wide, or of one layer."""
+        c = self.counters.cpu().numpy()
+        if layer is None:
+            return {"last_stamp": int(c[0]), "hits": int(c[1]), "misses": int(c[2]), "routed_hits": int(c[3])}
+        r = c[4 + 4 * layer: 8 + 4 * layer]
+        return {"hits": int(r[0]), "misses": int(r[1]), "routed_hits": int(r[2]), "routed": int(r[3])}
+
+    def state(self):
+        """(slot table [layers, experts], owners [slots], stamps [slots]) on the host."""
+        return (self.pool.slot_table.cpu().numpy(), self.slot_owner.cpu().numpy(),
+                self.slot_stamp.cpu().numpy().view(np.uint64))
+
+
 def route_words(slots_of: dict, routed) -> np.ndarray:
     """``SLOT_BIT | slot`` for every routed expert (expert_cache.py:1915-1917)."""
     return np.array([SLOT_BIT | slots_of[int(e)] for e in routed], dtype=np.uint32)
 
 
-__all__ = ["ExpertPool", "HostRecordStore", "PARTS", "SLOT_BIT", "route_words"]
+__all__ = ["DeviceLru", "ExpertPool", "HostRecordStore", "PARTS", "SLOT_BIT", "restore_from_stamps",
+           "route_words", "stamp_state"]
