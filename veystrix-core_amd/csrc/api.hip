@@ -362,15 +362,17 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
 
 // Workspace of the grouped path (more than VM_LAYER_MAX_TOKENS rows).
 struct GroupedWs {
-  uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, row_token, pair_row, act, rows, total;
-  uint32_t rows_total, groups, max_tiles;
+  uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, tiles_dn, tile_count_dn, row_token, pair_row,
+      act, rows, total;
+  uint32_t rows_total, groups, max_tiles, max_tiles_dn;
 };
 
 static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint32_t E, bool shared) {
   GroupedWs w{};
   w.rows_total = T * K + (shared ? T : 0);
   w.groups = E + (shared ? 1 : 0);
-  w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups);
+  w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups, vm::kGroupedRows);
+  w.max_tiles_dn = vm::grouped_max_tiles(w.rows_total, w.groups, vm::kGroupedRowsDown);
   uint64_t o = kAlign;
   auto take = [&](uint64_t bytes) {
     const uint64_t at = o;
@@ -384,6 +386,8 @@ static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint
   w.row_off = take(uint64_t(w.groups + 1) * 4);
   w.tiles = take(uint64_t(w.max_tiles) * 8);
   w.tile_count = take(4);
+  w.tiles_dn = take(uint64_t(w.max_tiles_dn) * 8);
+  w.tile_count_dn = take(4);
   w.row_token = take(uint64_t(w.rows_total) * 4);
   w.pair_row = take(uint64_t(T) * K * 4);
   w.act = take(uint64_t(w.rows_total) * I * 2);
@@ -700,6 +704,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   s.row_off = reinterpret_cast<uint32_t*>(ws + w.row_off);
   s.tiles = reinterpret_cast<uint2*>(ws + w.tiles);
   s.tile_count = reinterpret_cast<uint32_t*>(ws + w.tile_count);
+  s.tiles_dn = reinterpret_cast<uint2*>(ws + w.tiles_dn);
+  s.tile_count_dn = reinterpret_cast<uint32_t*>(ws + w.tile_count_dn);
   s.row_token = reinterpret_cast<uint32_t*>(ws + w.row_token);
   s.pair_row = reinterpret_cast<uint32_t*>(ws + w.pair_row);
   s.status = g.status;
@@ -747,7 +753,9 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.k_dim = g.I;
   q.n_dim = g.H;
   q.a_stride = g.I;
-  e = vm::launch_grouped(vm::kEpiRows, q, w.max_tiles, stream);
+  q.tiles = s.tiles_dn;
+  q.tile_count = s.tile_count_dn;
+  e = vm::launch_grouped(vm::kEpiRows, q, w.max_tiles_dn, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped down launch");
 
   vm::CombineLaunch c{};

@@ -41,8 +41,6 @@ namespace vm {
 namespace {
 
 constexpr int kGB = 256;                 // threads per block of the small kernels
-constexpr int kBM = kGroupedRows;        // rows per tile
-constexpr int kMB = kBM / 16;            // MFMA row blocks
 #ifndef VM_GCG
 #define VM_GCG 8
 #endif
@@ -50,7 +48,6 @@ constexpr int kCG = VM_GCG;              // 32-input groups per K chunk (8: a 12
 constexpr int kHalves = kCG / 4;         // groups per lane and chunk
 constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
 constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
-constexpr int kStageBytes = kBM * kRowBytes;
 
 // Bytes of one LDS stage of a grouped GEMM instance: the A rows, then for Q4
 // weights without a tail chunk the chunk's scale and bias vectors of every
@@ -58,18 +55,29 @@ constexpr int kStageBytes = kBM * kRowBytes;
 #ifndef VM_LDS_B
 #define VM_LDS_B 1
 #endif
+// the down GEMM (K = the intermediate size, two chunks) loads its weights
+// straight into the MFMA lanes: without the weight stage two blocks fit per CU
+#ifndef VM_LDS_B_DN
+#define VM_LDS_B_DN 0
+#endif
 constexpr int kWColBytes = kCG * 16 + 16;  // LDS bytes per staged weight row chunk (+16 against bank conflicts)
 
 // Q4 weights staged through LDS (coalesced 128-byte row loads by the whole
 // block) rather than loaded by the MFMA lanes themselves.
 template <int EPI, bool TAIL>
 constexpr bool lds_weights() {
-  return VM_LDS_B && EPI != kEpiLogits && !TAIL;
+  return (EPI == kEpiRows ? VM_LDS_B_DN : VM_LDS_B) && EPI != kEpiLogits && !TAIL;
+}
+
+// Rows per tile of a grouped GEMM instance.
+template <int EPI>
+constexpr int tile_rows() {
+  return EPI == kEpiRows ? kGroupedRowsDown : kGroupedRows;
 }
 
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 constexpr int stage_bytes() {
-  return kStageBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
+  return tile_rows<EPI>() * kRowBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
          (lds_weights<EPI, TAIL>() ? PROJ * WAVES * NBW * 16 * kWColBytes : 0);
 }
 
@@ -263,6 +271,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr int kSVecs = kLdsScales ? PROJ * 2 * kCols : 0;
   constexpr int kSItems = (kSVecs + kThreads - 1) / kThreads;
   constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
+  constexpr int kStageBytes = tile_rows<EPI>() * kRowBytes;  // the A rows of a stage
   const uint16_t* sv_src[kSItems > 0 ? kSItems : 1];
 #pragma unroll
   for (int j = 0; j < kSItems; ++j) {
@@ -478,9 +487,15 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #ifndef VM_G_WAVES_PER_EU
 #define VM_G_WAVES_PER_EU 1
 #endif
+#ifndef VM_DN_WAVES_PER_EU
+#define VM_DN_WAVES_PER_EU 2
+#endif
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
-__global__ __launch_bounds__(WAVES * 64) __attribute__((amdgpu_waves_per_eu(VM_G_WAVES_PER_EU)))
+__global__ __launch_bounds__(WAVES * 64)
+__attribute__((amdgpu_waves_per_eu(EPI == kEpiRows ? VM_DN_WAVES_PER_EU : VM_G_WAVES_PER_EU)))
 void k_grouped(GroupedLaunch p) {
+  constexpr int kBM = tile_rows<EPI>();
+  constexpr int kMB = kBM / 16;  // MFMA row blocks
   static_assert(kBM % 16 == 0 && kBM <= 64, "tiles are one to four 16-row blocks");
   constexpr bool Q4 = EPI != kEpiLogits;
   extern __shared__ uint4 s_dyn[];  // two stages of stage_bytes<...>()
@@ -569,8 +584,9 @@ __device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
 }
 
 // The whole sort in one block: LDS histogram of the routes, scan into row
-// offsets and the tile list (group, first row) of kBM-row tiles, LDS cursors,
-// scatter.  groups = experts (+1 for the shared rows) <= 1024.
+// offsets and two tile lists (group, first row), one of gate/up tiles and one
+// of down tiles, LDS cursors, scatter.  groups = experts (+1 for the shared
+// rows) <= 1024.
 // BATCH pair ids per thread are loaded together (clamped, unconditional), so
 // each batch costs one load latency rather than one per pair; small calls use
 // BATCH = 1 (no clamped duplicates).
@@ -603,17 +619,21 @@ __global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
   uint32_t n = 0;
   if (g < p.experts) n = s_count[g];
   else if (g < groups) n = p.shared_rows;
-  const uint32_t nt = (n + kBM - 1) / kBM;
+  const uint32_t nt = (n + kGroupedRows - 1) / kGroupedRows;
+  const uint32_t nt_dn = (n + kGroupedRowsDown - 1) / kGroupedRowsDown;
   const uint32_t row_end = block_scan_1024(n, s_wave);
   const uint32_t tile_end = block_scan_1024(nt, s_wave);
-  const uint32_t row_begin = row_end - n, tile_begin = tile_end - nt;
+  const uint32_t tile_end_dn = block_scan_1024(nt_dn, s_wave);
+  const uint32_t row_begin = row_end - n, tile_begin = tile_end - nt, tile_begin_dn = tile_end_dn - nt_dn;
   if (g < groups) {
     p.row_off[g] = row_begin;
-    for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * kBM);
+    for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * kGroupedRows);
+    for (uint32_t i = 0; i < nt_dn; ++i) p.tiles_dn[tile_begin_dn + i] = make_uint2(g, i * kGroupedRowsDown);
   }
   if (g == groups - 1) {
     p.row_off[groups] = row_end;
     *p.tile_count = tile_end;
+    *p.tile_count_dn = tile_end_dn;
   }
   if (g == p.experts) s_shared_first = row_begin;
   s_count[g] = row_begin;  // scatter cursors
@@ -764,7 +784,9 @@ hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_t
 
 }  // namespace
 
-uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups) { return (rows + kBM - 1) / kBM + groups; }
+uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups, uint32_t tile_rows) {
+  return (rows + tile_rows - 1) / tile_rows + groups;
+}
 
 // block shapes (waves, 16-column blocks per wave) of the gate/up and down GEMMs
 #ifndef VM_GU_WAVES

@@ -119,7 +119,14 @@ hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 #ifndef VM_GROUPED_ROWS
 #define VM_GROUPED_ROWS 64
 #endif
-constexpr int kGroupedRows = VM_GROUPED_ROWS;  // rows per grouped GEMM tile (16, 32, 48 or 64)
+#ifndef VM_GROUPED_ROWS_DN
+#define VM_GROUPED_ROWS_DN 48
+#endif
+// rows per grouped GEMM tile (16, 32, 48 or 64): gate/up (and the router
+// GEMM), and the down projection, whose short K (the intermediate size) runs
+// best with more, shorter tiles at two blocks per CU
+constexpr int kGroupedRows = VM_GROUPED_ROWS;
+constexpr int kGroupedRowsDown = VM_GROUPED_ROWS_DN;
 constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
 enum : int { kEpiSwiglu = 0, kEpiRows = 1, kEpiLogits = 2 };
 
@@ -148,8 +155,10 @@ struct GroupedLaunch {
 struct SortLaunch {
   const int32_t* inds;         // [tokens, slots]
   uint32_t* row_off;           // [groups + 1]
-  uint2* tiles;
+  uint2* tiles;                // kGroupedRows-row tiles (gate/up)
   uint32_t* tile_count;
+  uint2* tiles_dn;             // kGroupedRowsDown-row tiles (down)
+  uint32_t* tile_count_dn;
   uint32_t* row_token;         // [rows]
   uint32_t* pair_row;          // [tokens * slots]
   uint32_t* status;
@@ -169,7 +178,8 @@ struct CombineLaunch {
   int mode;                    // 0 fused combine, 1 generic combine, 2 per-slot rows
 };
 
-uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups);
+// Upper bound of the tiles of `tile_rows` rows over `groups` groups holding `rows` rows.
+uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups, uint32_t tile_rows);
 hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream);
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream);
