@@ -45,6 +45,10 @@ constexpr int kGB = 256;                 // threads per block of the small kerne
 #define VM_GCG 8
 #endif
 constexpr int kCG = VM_GCG;              // 32-input groups per K chunk (8: a 128-byte line per weight row)
+// A chunk's scale and bias vectors are staged with one 16-byte load of eight
+// groups from the chunk's first group, and full (non-tail) kernels need K to be
+// a multiple of the chunk: any other chunk size would read past the row.
+static_assert(kCG == 8, "the scale and bias staging covers exactly eight groups per chunk");
 constexpr int kHalves = kCG / 4;         // groups per lane and chunk
 constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
 constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
