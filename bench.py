@@ -22,7 +22,9 @@ sample of tokens, on this host's cores.
 Extra fields (not `value`): "batched" (32 rows per call, Zipf(1.1) routing,
 8 pool-resident layers cycled) and "prefill" (2048 rows per call, 3 layers
 cycled) through the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA
-fraction (algorithmic FLOPs / time / 2.5 PFLOP/s); "stack48_lru" (48 layers at
+fraction (algorithmic FLOPs / time / 2.5 PFLOP/s); "prefill_window" (the
+layer-major order: four 2048-row chunks in one layer call, each expert read
+once per window); "stack48_lru" (48 layers at
 batch 1 with a 3,051-slot LRU pool, Zipf routing, misses staged from pinned
 host memory): tokens/s through the stack, hit rate, staged bytes.
 """
@@ -461,6 +463,9 @@ def main():
         result["batched"] = run_grouped("batched", 32, 8, 50, args.seed)
         log("chunked prefill: 2048 rows")
         result["prefill"] = run_grouped("prefill", 2048, 3, 8, args.seed)
+        log("layer-major prefill window: four 2048-row chunks per layer call")
+        result["prefill_window"] = run_grouped("prefill", 8192, 3, 4, args.seed)
+        result["prefill_window"]["window"] = "4 chunks x 2048 rows in one layer call (layer-major order)"
     if not args.no_stack:
         log("48-layer stack, LRU pool of 6 GB, misses from pinned host")
         # the stated Zipf(1.1) recipe, and its logit bias scaled to reach the ~60% hit rate
