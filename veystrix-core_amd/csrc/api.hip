@@ -362,8 +362,8 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
 
 // Workspace of the grouped path (more than VM_LAYER_MAX_TOKENS rows).
 struct GroupedWs {
-  uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, tiles_dn, tile_count_dn, row_token, pair_row,
-      act, rows, total;
+  uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, tiles_dn, tile_count_dn, sort_counts,
+      sort_cursors, row_token, pair_row, act, rows, total;
   uint32_t rows_total, groups, max_tiles, max_tiles_dn;
 };
 
@@ -388,6 +388,8 @@ static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint
   w.tile_count = take(4);
   w.tiles_dn = take(uint64_t(w.max_tiles_dn) * 8);
   w.tile_count_dn = take(4);
+  w.sort_counts = take(1024 * 4);
+  w.sort_cursors = take(1024 * 4);
   w.row_token = take(uint64_t(w.rows_total) * 4);
   w.pair_row = take(uint64_t(T) * K * 4);
   w.act = take(uint64_t(w.rows_total) * I * 2);
@@ -706,6 +708,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   s.tile_count = reinterpret_cast<uint32_t*>(ws + w.tile_count);
   s.tiles_dn = reinterpret_cast<uint2*>(ws + w.tiles_dn);
   s.tile_count_dn = reinterpret_cast<uint32_t*>(ws + w.tile_count_dn);
+  s.counts = reinterpret_cast<uint32_t*>(ws + w.sort_counts);
+  s.cursors = reinterpret_cast<uint32_t*>(ws + w.sort_cursors);
   s.row_token = reinterpret_cast<uint32_t*>(ws + w.row_token);
   s.pair_row = reinterpret_cast<uint32_t*>(ws + w.pair_row);
   s.status = g.status;

@@ -587,42 +587,12 @@ __device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
   return v + before;
 }
 
-// The whole sort in one block: LDS histogram of the routes, scan into row
-// offsets and two tile lists (group, first row), one of gate/up tiles and one
-// of down tiles, LDS cursors, scatter.  groups = experts (+1 for the shared
-// rows) <= 1024.
-// BATCH pair ids per thread are loaded together (clamped, unconditional), so
-// each batch costs one load latency rather than one per pair; small calls use
-// BATCH = 1 (no clamped duplicates).
-template <int BATCH>
-__global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
-  constexpr int kSortBatch = BATCH;
-  __shared__ uint32_t s_count[1024];
-  __shared__ uint32_t s_wave[16];
-  __shared__ uint32_t s_shared_first;
+// Row offsets, both tile lists (group, first row) of the gate/up and the down
+// tiles, from the row count n of group g = threadIdx.x (one block of 1024
+// threads).  Returns the group's first row.
+__device__ uint32_t sort_layout(const SortLaunch& p, uint32_t n, uint32_t* s_wave) {
   const uint32_t g = threadIdx.x;
-  const uint32_t pairs = p.tokens * p.slots;
   const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
-  s_count[g] = 0;
-  __syncthreads();
-  auto load_batch = [&](uint32_t base, uint32_t (&e)[kSortBatch]) {
-#pragma unroll
-    for (int j = 0; j < kSortBatch; ++j) e[j] = static_cast<uint32_t>(p.inds[min(base + j * 1024 + g, pairs - 1)]);
-  };
-  for (uint32_t base = 0; base < pairs; base += 1024 * kSortBatch) {
-    uint32_t e[kSortBatch];
-    load_batch(base, e);
-#pragma unroll
-    for (int j = 0; j < kSortBatch; ++j) {
-      if (base + j * 1024 + g >= pairs) continue;
-      if (e[j] < p.experts) atomicAdd(&s_count[e[j]], 1u);
-      else flag(p.status, 2u);
-    }
-  }
-  __syncthreads();
-  uint32_t n = 0;
-  if (g < p.experts) n = s_count[g];
-  else if (g < groups) n = p.shared_rows;
   const uint32_t nt = (n + kGroupedRows - 1) / kGroupedRows;
   const uint32_t nt_dn = (n + kGroupedRowsDown - 1) / kGroupedRowsDown;
   const uint32_t row_end = block_scan_1024(n, s_wave);
@@ -639,26 +609,129 @@ __global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
     *p.tile_count = tile_end;
     *p.tile_count_dn = tile_end_dn;
   }
+  return row_begin;
+}
+
+// The whole sort in one block (small calls): LDS histogram of the routes, the
+// layout (sort_layout), LDS cursors, scatter.  groups = experts (+1 for the
+// shared rows) <= 1024.
+__global__ __launch_bounds__(1024) void k_sort(SortLaunch p) {
+  __shared__ uint32_t s_count[1024];
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_shared_first;
+  const uint32_t g = threadIdx.x;
+  const uint32_t pairs = p.tokens * p.slots;
+  const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
+  s_count[g] = 0;
+  __syncthreads();
+  for (uint32_t i = g; i < pairs; i += 1024) {
+    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
+    if (e < p.experts) atomicAdd(&s_count[e], 1u);
+    else flag(p.status, 2u);
+  }
+  __syncthreads();
+  uint32_t n = 0;
+  if (g < p.experts) n = s_count[g];
+  else if (g < groups) n = p.shared_rows;
+  const uint32_t row_begin = sort_layout(p, n, s_wave);
   if (g == p.experts) s_shared_first = row_begin;
   s_count[g] = row_begin;  // scatter cursors
   __syncthreads();
-  for (uint32_t base = 0; base < pairs; base += 1024 * kSortBatch) {
-    uint32_t e[kSortBatch];
-    load_batch(base, e);
-#pragma unroll
-    for (int j = 0; j < kSortBatch; ++j) {
-      const uint32_t i = base + j * 1024 + g;
-      if (i >= pairs) continue;
-      if (e[j] < p.experts) {
-        const uint32_t pos = atomicAdd(&s_count[e[j]], 1u);
-        p.row_token[pos] = i / p.slots;
-        p.pair_row[i] = pos;
-      } else {
-        p.pair_row[i] = kNoRow;
-      }
+  for (uint32_t i = g; i < pairs; i += 1024) {
+    const uint32_t e = static_cast<uint32_t>(p.inds[i]);
+    if (e < p.experts) {
+      const uint32_t pos = atomicAdd(&s_count[e], 1u);
+      p.row_token[pos] = i / p.slots;
+      p.pair_row[i] = pos;
+    } else {
+      p.pair_row[i] = kNoRow;
     }
   }
   for (uint32_t i = g; i < p.shared_rows; i += 1024) p.row_token[s_shared_first + i] = i;
+}
+
+// The sort of large calls over many blocks (the scattered row writes of one
+// block were the cost): zero the counts, per-block LDS histograms added to
+// global counts, one block lays out rows and tiles, then every block reserves
+// each expert's run of rows with one atomic and scatters its pairs into it.
+// The order of an expert's rows then depends on which block reserved first,
+// which changes no result: every output row is its own set of dot products.
+constexpr int kSortThreads = 256;
+constexpr int kSortPerThread = 8;
+constexpr uint32_t kSortBlockPairs = kSortThreads * kSortPerThread;
+
+__global__ __launch_bounds__(1024) void k_sort_zero(SortLaunch p) { p.counts[threadIdx.x] = 0; }
+
+__global__ __launch_bounds__(kSortThreads) void k_sort_count(SortLaunch p) {
+  __shared__ uint32_t s_count[1024];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t pairs = p.tokens * p.slots;
+  const uint32_t base = blockIdx.x * kSortBlockPairs;
+  for (uint32_t g = tid; g < 1024; g += kSortThreads) s_count[g] = 0;
+  __syncthreads();
+  uint32_t e[kSortPerThread];
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j)
+    e[j] = static_cast<uint32_t>(p.inds[min(base + j * kSortThreads + tid, pairs - 1)]);
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j) {
+    if (base + j * kSortThreads + tid >= pairs) continue;
+    if (e[j] < p.experts) atomicAdd(&s_count[e[j]], 1u);
+    else flag(p.status, 2u);
+  }
+  __syncthreads();
+  for (uint32_t g = tid; g < p.experts; g += kSortThreads)
+    if (s_count[g] != 0) atomicAdd(&p.counts[g], s_count[g]);
+}
+
+__global__ __launch_bounds__(1024) void k_sort_scan(SortLaunch p) {
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_shared_first;
+  const uint32_t g = threadIdx.x;
+  const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
+  uint32_t n = 0;
+  if (g < p.experts) n = p.counts[g];
+  else if (g < groups) n = p.shared_rows;
+  const uint32_t row_begin = sort_layout(p, n, s_wave);
+  if (g == p.experts) s_shared_first = row_begin;
+  p.cursors[g] = row_begin;
+  __syncthreads();
+  for (uint32_t i = g; i < p.shared_rows; i += 1024) p.row_token[s_shared_first + i] = i;
+}
+
+__global__ __launch_bounds__(kSortThreads) void k_sort_scatter(SortLaunch p) {
+  __shared__ uint32_t s_count[1024];
+  __shared__ uint32_t s_base[1024];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t pairs = p.tokens * p.slots;
+  const uint32_t base = blockIdx.x * kSortBlockPairs;
+  for (uint32_t g = tid; g < 1024; g += kSortThreads) s_count[g] = 0;
+  __syncthreads();
+  uint32_t e[kSortPerThread], local[kSortPerThread];
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j)
+    e[j] = static_cast<uint32_t>(p.inds[min(base + j * kSortThreads + tid, pairs - 1)]);
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j) {
+    local[j] = 0;
+    if (base + j * kSortThreads + tid < pairs && e[j] < p.experts) local[j] = atomicAdd(&s_count[e[j]], 1u);
+  }
+  __syncthreads();
+  for (uint32_t g = tid; g < p.experts; g += kSortThreads)
+    if (s_count[g] != 0) s_base[g] = atomicAdd(&p.cursors[g], s_count[g]);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kSortPerThread; ++j) {
+    const uint32_t i = base + j * kSortThreads + tid;
+    if (i >= pairs) continue;
+    if (e[j] < p.experts) {
+      const uint32_t pos = s_base[e[j]] + local[j];
+      p.row_token[pos] = i / p.slots;
+      p.pair_row[i] = pos;
+    } else {
+      p.pair_row[i] = kNoRow;
+    }
+  }
 }
 
 // --------------------------------------------------------------- combine ---
@@ -815,9 +888,18 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
   }
 }
 
+// Calls up to this many (token, slot) pairs sort in one block.
+constexpr uint32_t kSortOneBlockPairs = 4096;
+
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
-  if (p.tokens * p.slots > 16384) return launch("sort", k_sort<16>, dim3(1), dim3(1024), stream, p);
-  return launch("sort", k_sort<1>, dim3(1), dim3(1024), stream, p);
+  const uint32_t pairs = p.tokens * p.slots;
+  if (pairs <= kSortOneBlockPairs) return launch("sort", k_sort, dim3(1), dim3(1024), stream, p);
+  const dim3 blocks((pairs + kSortBlockPairs - 1) / kSortBlockPairs);
+  hipError_t e = launch("sort", k_sort_zero, dim3(1), dim3(1024), stream, p);
+  if (e == hipSuccess) e = launch("sort", k_sort_count, blocks, dim3(kSortThreads), stream, p);
+  if (e == hipSuccess) e = launch("sort", k_sort_scan, dim3(1), dim3(1024), stream, p);
+  if (e == hipSuccess) e = launch("sort", k_sort_scatter, blocks, dim3(kSortThreads), stream, p);
+  return e;
 }
 
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {

@@ -159,6 +159,8 @@ struct SortLaunch {
   uint32_t* tile_count;
   uint2* tiles_dn;             // kGroupedRowsDown-row tiles (down)
   uint32_t* tile_count_dn;
+  uint32_t* counts;            // [1024] scratch of the multi-block sort: rows per group
+  uint32_t* cursors;           // [1024] scratch of the multi-block sort: next free row per group
   uint32_t* row_token;         // [rows]
   uint32_t* pair_row;          // [tokens * slots]
   uint32_t* status;
