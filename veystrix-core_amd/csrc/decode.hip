@@ -461,10 +461,17 @@ struct RouterChunk<ActF32> {
   }
 };
 
-// One router row per wave.  CH = 16-byte chunks per lane per row (hidden/512,
-// rounded up).  With a single token its activations stay in registers.
-template <class A, int CH>
-__device__ void router_row(const FrontLaunch& p, uint32_t row, uint32_t lane) {
+// Tokens per row of router blocks (grid y), and tokens whose activations a
+// router wave loads together before their dot products.
+constexpr uint32_t kFrontTokens = 8;
+constexpr int kFrontUnroll = 4;
+
+// One router row per wave over tokens [t_begin, t_end).  CH = 16-byte chunks
+// per lane per row (hidden/512, rounded up).  U tokens at a time: their loads
+// are issued together (tokens past the end repeat the last one and are not
+// stored), so a row costs one load latency per U tokens.
+template <class A, int CH, int U>
+__device__ void router_row(const FrontLaunch& p, uint32_t row, uint32_t lane, uint32_t t_begin, uint32_t t_end) {
   const uint32_t H = p.hidden;
   uint4 w[CH];
 #pragma unroll
@@ -473,57 +480,75 @@ __device__ void router_row(const FrontLaunch& p, uint32_t row, uint32_t lane) {
     w[c] = e8 < H ? *reinterpret_cast<const uint4*>(p.weight + static_cast<size_t>(row) * H + e8)
                   : make_uint4(0, 0, 0, 0);
   }
-  for (uint32_t t = 0; t < p.tokens; ++t) {
-    float acc = 0.0f;
+  for (uint32_t t0 = t_begin; t0 < t_end; t0 += U) {
+    float acc[U];
 #pragma unroll
-    for (int c = 0; c < CH; ++c) {
-      const uint32_t e8 = 8 * (lane + 64 * c);
-      RouterChunk<A> xc;
-      if (e8 < H) xc.load(p.x, static_cast<size_t>(t) * H + e8); else xc.zero();
-      acc = xc.dot(w[c], acc);
+    for (int u = 0; u < U; ++u) {
+      const uint32_t t = min(t0 + u, t_end - 1);
+      acc[u] = 0.0f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const uint32_t e8 = 8 * (lane + 64 * c);
+        RouterChunk<A> xc;
+        if (e8 < H) xc.load(p.x, static_cast<size_t>(t) * H + e8); else xc.zero();
+        acc[u] = xc.dot(w[c], acc[u]);
+      }
     }
-    acc = group_sum<64>(acc);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] = group_sum<64>(acc[u]);
     if (lane == 63) {
-      if (p.bias != nullptr) acc += p.bias[row];
-      p.logits[static_cast<size_t>(t) * p.experts + row] = A::round(acc);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (t0 + u >= t_end) break;
+        float v = acc[u];
+        if (p.bias != nullptr) v += p.bias[row];
+        p.logits[static_cast<size_t>(t0 + u) * p.experts + row] = A::round(v);
+      }
     }
   }
 }
 
-// The shared expert's H -> 1 quantized gate followed by the sigmoid.
+// The shared expert's H -> 1 quantized gate followed by the sigmoid, for one token.
 template <class A>
-__device__ void shared_gate_logit(const FrontLaunch& p, uint32_t lane) {
+__device__ void shared_gate_token(const FrontLaunch& p, uint32_t t, uint32_t lane) {
   const uint32_t H = p.hidden, G = H / kGroup;
-  for (uint32_t t = 0; t < p.tokens; ++t) {
-    float acc = 0.0f;
-    for (uint32_t g = lane; g < G; g += 64) {
-      const uint4 w = *reinterpret_cast<const uint4*>(p.seg.w + g * kWordsPerGroup);
-      GroupAct<A> xa;
-      xa.fetch(p.x, static_cast<size_t>(t) * H + g * kGroup);
-      xa.prepare();
-      acc += xa.apply(w, bf16_to_f32(p.seg.s[g]), bf16_to_f32(p.seg.b[g]));
-    }
-    const float logit = A::round(wave_sum_all(acc));
-    if (lane == 0) A::store(p.shared_sig, t, sigmoid_act<A>(logit));
+  float acc = 0.0f;
+  for (uint32_t g = lane; g < G; g += 64) {
+    const uint4 w = *reinterpret_cast<const uint4*>(p.seg.w + g * kWordsPerGroup);
+    GroupAct<A> xa;
+    xa.fetch(p.x, static_cast<size_t>(t) * H + g * kGroup);
+    xa.prepare();
+    acc += xa.apply(w, bf16_to_f32(p.seg.s[g]), bf16_to_f32(p.seg.b[g]));
   }
+  const float logit = A::round(wave_sum_all(acc));
+  if (lane == 0) A::store(p.shared_sig, t, sigmoid_act<A>(logit));
 }
 
+// Blocks [0, router_blocks): router rows, one per wave, for the kFrontTokens
+// tokens of grid row y; the blocks after them: the shared gate, one wave per
+// token of that row.
 template <class A, int CH>
 __global__ __launch_bounds__(kBlock) void k_front(FrontLaunch p, uint32_t router_blocks) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   PhaseTrace tr;
   if (p.trace != nullptr) tr.mark(0);
+  const uint32_t t_begin = blockIdx.y * kFrontTokens;
+  const uint32_t t_end = min(p.tokens, t_begin + kFrontTokens);
   if (blockIdx.x >= router_blocks) {
-    if (wave == 0) shared_gate_logit<A>(p, lane);
+    const uint32_t t = t_begin + (blockIdx.x - router_blocks) * kWaves + wave;
+    if (t < t_end) shared_gate_token<A>(p, t, lane);
   } else {
     const uint32_t row = blockIdx.x * kWaves + wave;
-    if (row < p.experts) router_row<A, CH>(p, row, lane);
+    if (row < p.experts) {
+      if (t_end - t_begin == 1) router_row<A, CH, 1>(p, row, lane, t_begin, t_end);
+      else router_row<A, CH, kFrontUnroll>(p, row, lane, t_begin, t_end);
+    }
   }
   if (p.trace != nullptr && threadIdx.x == 0) {
     tr.mark(1);
     tr.t[2] = tr.t[3] = tr.t[4] = tr.t[1];
-    tr.write(p.trace, 1, blockIdx.x);
+    tr.write(p.trace, 1, blockIdx.y * gridDim.x + blockIdx.x);
   }
 }
 
@@ -985,11 +1010,12 @@ hipError_t down_dispatch(const DownLaunch& p, hipStream_t stream) {
 template <class A>
 hipError_t front_go(const FrontLaunch& p0, hipStream_t stream) {
   const uint32_t router_blocks = (p0.experts + kWaves - 1) / kWaves;
-  const uint32_t blocks = router_blocks + (p0.seg.w != nullptr ? 1 : 0);
+  const uint32_t row_tokens = p0.tokens < kFrontTokens ? p0.tokens : kFrontTokens;
+  const uint32_t shared_blocks = p0.seg.w != nullptr ? (row_tokens + kWaves - 1) / kWaves : 0;
+  const dim3 grid(router_blocks + shared_blocks, (p0.tokens + kFrontTokens - 1) / kFrontTokens), block(kBlock);
   FrontLaunch p = p0;
-  p.trace = trace_reserve(blocks);
+  p.trace = trace_reserve(grid.x * grid.y);
   const uint32_t chunks = (p.hidden / 8 + 63) / 64;
-  const dim3 grid(blocks), block(kBlock);
   if (chunks <= 1) return launch("router", k_front<A, 1>, grid, block, stream, p, router_blocks);
   if (chunks <= 2) return launch("router", k_front<A, 2>, grid, block, stream, p, router_blocks);
   if (chunks <= 4) return launch("router", k_front<A, 4>, grid, block, stream, p, router_blocks);
