@@ -1,7 +1,7 @@
 """The device LRU's algorithm, pinned on the CPU against the reference-semantics
 LRU (oracle.pool_oracle.LruSlots, a restatement of expert_pool.py:123-159).
 
-``StampModel`` runs the steps of the device kernel k_lru_assign on numpy
+``StampModel`` runs the steps of the device LRU (lru_assign in vm_lru.h) on numpy
 arrays: distinct ids in first-seen order, hits stamped in that order, then the
 misses take the non-hit slots with the smallest stamps, oldest first.  It must
 hand out exactly the slots the OrderedDict LRU hands out, from a fresh pool and
@@ -20,7 +20,7 @@ LAYERS, EXPERTS = 6, 48
 
 
 class StampModel:
-    """k_lru_assign on the host: table [layers, experts], owner/stamp per slot."""
+    """The device assign on the host: table [layers, experts], owner/stamp per slot."""
 
     def __init__(self, table, owner, stamp, last):
         self.table = table.copy()

@@ -471,6 +471,22 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   return VM_OK;
 }
 
+// Router logits (and the shared expert's sigmoid gate) of a decode call.
+static hipError_t launch_layer_front(const VmLayerArgs* a, const LayerWs& w, char* ws, hipStream_t stream) {
+  vm::FrontLaunch f{};
+  f.x = a->x;
+  f.weight = a->router_weight;
+  f.bias = a->router_bias;
+  f.logits = reinterpret_cast<float*>(ws + w.logits);
+  if (a->shared_inter != 0) f.seg = to_ptrs(a->shared_expert_gate);
+  f.shared_sig = ws + w.sig;
+  f.tokens = a->tokens;
+  f.hidden = a->hidden_size;
+  f.experts = a->expert_count;
+  f.act_dtype = static_cast<int>(a->act_dtype);
+  return vm::launch_front(f, stream);
+}
+
 static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
   const bool shared = a->shared_inter != 0;
@@ -492,18 +508,7 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   hipError_t e = hipSuccess;
 
   if (phases & VM_PHASE_ROUTER) {
-    vm::FrontLaunch f{};
-    f.x = a->x;
-    f.weight = a->router_weight;
-    f.bias = a->router_bias;
-    f.logits = logits;
-    if (shared) f.seg = to_ptrs(a->shared_expert_gate);
-    f.shared_sig = ws + w.sig;
-    f.tokens = T;
-    f.hidden = H;
-    f.experts = E;
-    f.act_dtype = static_cast<int>(a->act_dtype);
-    e = vm::launch_front(f, stream);
+    e = launch_layer_front(a, w, ws, stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     if (!fused) {
       vm::SelectLaunch s{};
@@ -614,6 +619,8 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   if (lru->layer >= lru->layers) return fail(VM_EINVAL, "layer %u is outside 0..%u", lru->layer, lru->layers);
   if (lru->slots != a->pool.records)
     return fail(VM_EINVAL, "LRU slots (%u) must equal the pool records (%u)", lru->slots, a->pool.records);
+  if (lru->slots > vm::kLruMaxSlots)
+    return fail(VM_EUNSUPPORTED, "the device LRU holds at most %u slots", vm::kLruMaxSlots);
   if (uint64_t(T) * K > lru->slots || uint64_t(T) * K > vm::kLruMaxRouted)
     return fail(VM_EINVAL, "tokens * top_k = %u exceeds the pool or the %u routed ids of one call", T * K,
                 vm::kLruMaxRouted);
@@ -623,7 +630,8 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   int rc = validate_layer(&r);
   if (rc != VM_OK) return rc;
   const uint64_t bytes = record_end(a->pool, H, I);
-  if (bytes % 16 || lru->host_stride % 16 || lru->host_stride < bytes || a->pool.header_size % 16)
+  if (bytes % 16 || lru->host_stride % 16 || lru->host_stride < bytes || a->pool.header_size % 16 ||
+      bytes / 16 * vm::kLruMaxRouted >= (1ull << 32))
     return fail(VM_EINVAL, "records of %llu bytes need 16-byte aligned host rows of at least that size",
                 (unsigned long long)bytes);
   if (!aligned16(lru->host_store)) return fail(VM_EINVAL, "host_store must be 16-byte aligned");
@@ -635,14 +643,22 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
     return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
   char* ws = static_cast<char*>(a->workspace);
 
-  // 1. router logits, shared gate, softmax/top-k into inds/scores
-  r.phases = VM_PHASE_ROUTER;
-  rc = layer_decode(&r, stream);
-  if (rc != VM_OK) return rc;
-  // 2. assign() on the device state, 3. fill the misses from the host store
+  // 1. router logits and shared gate
+  hipError_t e = launch_layer_front(a, w, ws, stream);
+  if (e != hipSuccess) return hip_fail(e, "router launch");
+  // 2. softmax/top-k into inds/scores and assign() on the device state, one block
+  int32_t* inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
+  vm::SelectLaunch sel{};
+  sel.logits = reinterpret_cast<const float*>(ws + w.logits);
+  sel.inds = inds;
+  sel.scores = a->scores_out != nullptr ? a->scores_out : static_cast<void*>(ws + w.scores);
+  sel.tokens = T;
+  sel.experts = E;
+  sel.top_k = K;
+  sel.act_dtype = static_cast<int>(a->act_dtype);
+  sel.blend = a->renorm_blend;
   uint32_t* fill = reinterpret_cast<uint32_t*>(ws + w.fill);
   vm::LruLaunch l{};
-  l.inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<const int32_t*>(ws + w.inds);
   l.slot_table = lru->slot_table;
   l.slot_owner = lru->slot_owner;
   l.slot_stamp = lru->slot_stamp;
@@ -658,8 +674,8 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   l.layers = lru->layers;
   l.layer = lru->layer;
   l.slots = lru->slots;
-  hipError_t e = vm::launch_lru(l, stream);
-  if (e != hipSuccess) return hip_fail(e, "lru launch");
+  e = vm::launch_select_lru(sel, l, stream);
+  if (e != hipSuccess) return hip_fail(e, "select/lru launch");
   vm::FillLaunch f{};
   f.count = l.fill_count;
   f.src = l.fill_src;
@@ -822,7 +838,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     r.n_dim = E;
     r.a_stride = H;
     r.experts = E;
-    e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRows - 1) / vm::kGroupedRows, stream);
+    e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");
     if (shared) {
       e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T, H,

@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "vm_internal.h"
+#include "vm_lru.h"
 
 namespace vm {
 
@@ -416,6 +417,37 @@ __device__ void select_body(const SelectLaunch& p) {
 
 __global__ __launch_bounds__(64) void k_select_bf16(SelectLaunch p) { select_body<ActBF16>(p); }
 __global__ __launch_bounds__(64) void k_select_f32(SelectLaunch p) { select_body<ActF32>(p); }
+
+// A decode call over a device-LRU pool: wave t selects the experts of token t
+// (softmax, top-k, renormalised scores, as select_body), then the block
+// applies the LRU assign to the routed ids, tokens in order and slots in rank
+// order (vm_lru.h).
+template <class A>
+__global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruLaunch l) {
+  __shared__ typename Cand<A>::T s_cands[kLruWaves][kMaxCand];
+  __shared__ int32_t s_routed[kLruMaxRouted];
+  __shared__ LruShared sh;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  if (wave < p.tokens) {
+    const uint32_t t = wave;
+    GateKeys<A> g;
+    float lg[kMaxExpertsPerLane];
+    load_logits(p.logits + static_cast<size_t>(t) * p.experts, p.experts, lane, lg);
+    softmax_keys<A>(lg, p.experts, lane, g);
+    uint32_t e;
+    float score;
+    rank_selection<A>(g, p.top_k, p.blend, lane, s_cands[wave], e, score);
+    if (lane < p.top_k) {
+      const size_t o = static_cast<size_t>(t) * p.top_k + lane;
+      p.inds[o] = static_cast<int32_t>(e);
+      A::store(p.scores, o, score);
+      s_routed[o] = static_cast<int32_t>(e);
+    }
+  }
+  __syncthreads();
+  lru_assign(l, s_routed, sh);
+}
 
 // -------------------------------------------------------------- front -----
 
@@ -1036,6 +1068,12 @@ bool down_supported(uint32_t inter, uint32_t slots_total, int /*act_dtype*/) {
 
 hipError_t launch_front(const FrontLaunch& p, hipStream_t stream) {
   return p.act_dtype == 0 ? front_go<ActBF16>(p, stream) : front_go<ActF32>(p, stream);
+}
+
+hipError_t launch_select_lru(const SelectLaunch& p, const LruLaunch& l, hipStream_t stream) {
+  const dim3 grid(1), block(kLruThreads);
+  return p.act_dtype == 0 ? launch("lru", k_select_lru<ActBF16>, grid, block, stream, p, l)
+                          : launch("lru", k_select_lru<ActF32>, grid, block, stream, p, l);
 }
 
 hipError_t launch_select(const SelectLaunch& p, hipStream_t stream) {

@@ -76,7 +76,7 @@ constexpr bool lds_weights() {
 // Rows per tile of a grouped GEMM instance.
 template <int EPI>
 constexpr int tile_rows() {
-  return EPI == kEpiRows ? kGroupedRowsDown : kGroupedRows;
+  return EPI == kEpiRows ? kGroupedRowsDown : EPI == kEpiLogits ? kGroupedRowsRouter : kGroupedRows;
 }
 
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>

@@ -83,11 +83,13 @@ struct DownLaunch {
 
 // ------------------------------------------------------ device-side LRU --
 constexpr uint32_t kLruMaxRouted = 80;  // VM_LAYER_MAX_TOKENS * MAX_TOP_K
+constexpr int kLruThreads = 1024;       // one block runs the selection and the assign
+constexpr int kLruSlotsPerThread = 32;  // slot stamps each thread holds in registers
+constexpr uint32_t kLruMaxSlots = kLruThreads * kLruSlotsPerThread;
 constexpr uint32_t kNoRecord = 0xffffffffu;
 
 // assign() of one decode call on the device state (one block).
 struct LruLaunch {
-  const int32_t* inds;         // [routed] expert ids, tokens in order, slots in rank order
   int32_t* slot_table;         // [layers, experts]
   int32_t* slot_owner;         // [slots]
   uint64_t* slot_stamp;        // [slots]
@@ -112,7 +114,9 @@ struct FillLaunch {
   uint64_t header, stride, pool_records, record_bytes;
 };
 
-hipError_t launch_lru(const LruLaunch& p, hipStream_t stream);
+// Softmax/top-k of up to kLruWaves tokens and the LRU assign of their routed
+// ids, one block (decode.hip).
+hipError_t launch_select_lru(const SelectLaunch& p, const LruLaunch& l, hipStream_t stream);
 hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 
 // ---------------------------------------------------------- grouped path --
@@ -125,8 +129,12 @@ hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 // rows per grouped GEMM tile (16, 32, 48 or 64): gate/up (and the router
 // GEMM), and the down projection, whose short K (the intermediate size) runs
 // best with more, shorter tiles at two blocks per CU
+#ifndef VM_GROUPED_ROWS_RT
+#define VM_GROUPED_ROWS_RT 64
+#endif
 constexpr int kGroupedRows = VM_GROUPED_ROWS;
 constexpr int kGroupedRowsDown = VM_GROUPED_ROWS_DN;
+constexpr int kGroupedRowsRouter = VM_GROUPED_ROWS_RT;  // router GEMM tiles (no sort: rows in order)
 constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
 enum : int { kEpiSwiglu = 0, kEpiRows = 1, kEpiLogits = 2 };
 
