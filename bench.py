@@ -244,7 +244,8 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
     slots and stages the misses from pinned host records with hipMemcpyAsync
     on a side stream.  `device_lru`: the LRU state lives on the GPU and the
     misses are read by a kernel straight from the pinned records, so no layer
-    waits for the host.  The host store holds `store_records` distinct records
+    waits for the host and the timed tokens replay one captured HIP graph of
+    the 48 layers each (veymoe.graph.StepGraph).  The host store holds `store_records` distinct records
     aliased over the 24,576 (layer, expert) ids (the bytes moved per miss are
     the same).  `bias_scale` multiplies the log-Zipf logit bias (1 = the
     stated recipe)."""
@@ -302,10 +303,19 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
     for t in range(warm_tokens):
         for layer in range(spec.layers):
             layers[layer](x[t, layer:layer + 1])
+    step = None
+    if lru is not None:
+        # no layer waits for the host: a token's 48 layers are one graph replay
+        from veymoe.graph import StepGraph
+
+        step = StepGraph(layers, rows=1, device=device).capture()
     torch.cuda.synchronize()
     hits0, misses0, staged0 = counts()
     start = time.perf_counter()
     for t in range(warm_tokens, warm_tokens + tokens):
+        if step is not None:
+            step.replay(x[t, :, None, :])
+            continue
         for layer in range(spec.layers):
             layers[layer](x[t, layer:layer + 1])
     torch.cuda.synchronize()
@@ -320,7 +330,8 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
     dst.copy_(big, non_blocking=True)
     torch.cuda.synchronize()
     h2d = big.numel() / (time.perf_counter() - t0) / 1e9
-    result = {"lru": "device" if device_lru else "host", "tokens": tokens, "layers": spec.layers,
+    result = {"lru": "device" if device_lru else "host", "launch": "hipgraph" if step is not None else "eager",
+              "tokens": tokens, "layers": spec.layers,
               "bias_scale": bias_scale,
               "tok_s": round(tokens / elapsed, 2),
               "ms_per_token": round(elapsed * 1e3 / tokens, 3), "pool_slots": pool.slots,
@@ -329,7 +340,7 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
               "staged_gbps": round(staged / elapsed / 1e9, 2), "pinned_h2d_gbps": round(h2d, 2),
               "host_store": f"{store_records} distinct pinned records ({store_records * layout.record_stride / 1e9:.1f} GB) "
                             f"aliased over {spec.layers * spec.experts} (layer, expert) ids"}
-    del layers, pool, store, x, big, dst
+    del layers, pool, store, x, big, dst, step
     torch.cuda.empty_cache()
     return result
 

@@ -214,33 +214,40 @@ typedef struct VmLayerArgs {
  * move to the most recent end in that order; then each miss, in that order,
  * takes the next victim: free slots first (in the order the reference's free
  * list pops them), then the least recently used key, whose table entry is
- * cleared.  Recency is a per-slot stamp: every slot carries a distinct stamp,
- * free slots the smallest, and the victims of a call are the slots with the
- * smallest stamps that are not hits of that call.
+ * cleared.  Recency is one queue of slot ids, lru_order: the free slots in
+ * pop order, then the resident slots from least to most recently used (the
+ * reference's free list followed by its OrderedDict).  A call's victims are
+ * the first misses-many entries of the queue that are not hits; the queue
+ * then holds the remaining non-hit entries, the hits in first-seen order and
+ * the victims in miss order.
  *
  * State (device memory owned by the caller, updated in place):
  *   slot_table  [layers, expert_count] int32: expert -> slot, -1 = absent
  *               (row `layer` replaces VmLayerArgs.slot_table, which is ignored)
  *   slot_owner  [slots] int32: layer * expert_count + expert, -1 = free
- *   slot_stamp  [slots] uint64, all distinct and nonzero
- *   counters    [4 + 4 * layers] uint64: last stamp issued, distinct hits,
- *               distinct misses, routed hits (routed positions minus distinct
- *               misses, the reference's StreamingSwitchGLU.hits); then per
- *               layer: distinct hits, distinct misses, routed hits, routed ids
+ *   lru_order   [order_len] int32: every candidate slot once (slots outside
+ *               the queue are never handed out)
+ *   counters    [4 + 4 * layers] uint64: distinct ids assigned (hits plus
+ *               misses), distinct hits, distinct misses, routed hits (routed
+ *               positions minus distinct misses, the reference's
+ *               StreamingSwitchGLU.hits); then per layer: distinct hits,
+ *               distinct misses, routed hits, routed ids
  *   host_row    [layers, expert_count] int32: row of the expert's record in
  *               host_store (-1: no record)
  *   host_store  pinned host memory (hipHostMalloc), host_records rows of
  *               host_stride bytes; rows are read by the GPU over the host link
- * slots must equal VmLayerArgs.pool.records and be at least tokens * top_k.
- * A miss whose expert has no host record is left unfilled and sets status bit
- * 4; a routed id outside 0..expert_count-1 is skipped and sets status bit 8;
- * a state with fewer candidate slots than misses (stamps not distinct or
- * zero) maps only the misses it can and sets status bit 16.  Calls that
- * overlap on one state race: issue them on one stream. */
+ * slots must equal VmLayerArgs.pool.records, order_len must be at most slots
+ * and at least tokens * top_k.  A miss whose expert has no host record is left
+ * unfilled and sets status bit 4; a routed id outside 0..expert_count-1 is
+ * skipped and sets status bit 8.  Status bit 16: a queue with an entry outside
+ * 0..slots-1 or without every hit slot exactly once leaves the state unchanged
+ * (nothing mapped, nothing filled); a queue with fewer non-hit entries than
+ * misses maps only the misses it can.  Calls that overlap on one state race:
+ * issue them on one stream. */
 typedef struct VmDeviceLru {
   int32_t* slot_table;
   int32_t* slot_owner;
-  uint64_t* slot_stamp;
+  int32_t* lru_order;
   uint64_t* counters;
   const int32_t* host_row;
   const void* host_store;
@@ -249,7 +256,7 @@ typedef struct VmDeviceLru {
   uint32_t layers;
   uint32_t layer;
   uint32_t slots;
-  uint32_t reserved;
+  uint32_t order_len;
 } VmDeviceLru;
 
 /* vm_moe_grouped: the expert block of the grouped path for any token count

@@ -47,3 +47,19 @@ def ulp_diff_bf16(a, b):
     ia = mo.f32_to_bf16_bits(np.asarray(a, np.float32)).astype(np.int32)
     ib = mo.f32_to_bf16_bits(np.asarray(b, np.float32)).astype(np.int32)
     return np.abs(ia - ib)
+
+
+def pooled_stack(device, spec, layers, slots, seed):
+    """A pinned host store with every (layer, expert) record of ``spec``, an
+    empty pool of ``slots`` records, pool-backed layers over it and the same
+    layers with dense weights: (store, pool, pooled, dense)."""
+    from veymoe.pool import ExpertPool, HostRecordStore
+
+    store = HostRecordStore(spec.layout, layers * spec.experts)
+    for layer in range(layers):
+        for expert in range(spec.experts):
+            store.put(layer, expert, synth.expert_record(spec, seed, layer, expert))
+    pool = ExpertPool(spec.layout, slots, layers=layers, experts=spec.experts, device=device)
+    pooled = [assemble.build_layer(spec, seed, device, layer=l, pool=pool, host_store=store) for l in range(layers)]
+    dense = [assemble.build_layer(spec, seed, device, layer=l, dense=True) for l in range(layers)]
+    return store, pool, pooled, dense

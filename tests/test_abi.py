@@ -110,9 +110,9 @@ def _lru_call(**kw):
     a.tokens, a.hidden_size, a.inter_size, a.expert_count, a.top_k, a.group_size = 1, 64, 64, 8, 2, 32
     a.pool.base, a.pool.record_stride, a.pool.records = 4096, 4096, 16
     lru = _lib.VmDeviceLru()
-    lru.slot_table, lru.slot_owner, lru.slot_stamp, lru.counters, lru.host_row = 1024, 1056, 1088, 1120, 1152
+    lru.slot_table, lru.slot_owner, lru.lru_order, lru.counters, lru.host_row = 1024, 1056, 1088, 1120, 1152
     lru.host_store, lru.host_stride, lru.host_records = 8192, 4096, 8
-    lru.layers, lru.layer, lru.slots = 2, 0, 16
+    lru.layers, lru.layer, lru.slots, lru.order_len = 2, 0, 16, 16
     for k, v in kw.items():
         target = lru if hasattr(lru, k) and k not in ("slot_table",) and not hasattr(a, k) else a
         setattr(target, k, v)
@@ -125,6 +125,9 @@ def _lru_call(**kw):
     ("host_store", None, _lib.VM_EINVAL, "state pointers"),
     ("layer", 2, _lib.VM_EINVAL, "outside"),
     ("slots", 15, _lib.VM_EINVAL, "must equal the pool records"),
+    ("lru_order", None, _lib.VM_EINVAL, "state pointers"),
+    ("order_len", 17, _lib.VM_EINVAL, "exceeds the slots"),
+    ("order_len", 1, _lib.VM_EINVAL, "queued slots"),
 ])
 def test_layer_lru_rejects_bad_arguments_without_a_device(field, value, code, message):
     assert _lru_call(**{field: value}) == code

@@ -8,9 +8,9 @@ import numpy as np
 import pytest
 import torch
 
+from gpu_util import pooled_stack
 from oracle import pool_oracle
 from veymoe import assemble, synth
-from veymoe.pool import ExpertPool, HostRecordStore
 
 pytestmark = pytest.mark.gpu
 
@@ -20,14 +20,7 @@ FULL = synth.LayerSpec("lru_full", 2048, 512, 64, 10, 512, 1)
 
 
 def _setup(device, spec, layers, slots):
-    store = HostRecordStore(spec.layout, layers * spec.experts)
-    for layer in range(layers):
-        for expert in range(spec.experts):
-            store.put(layer, expert, synth.expert_record(spec, SEED, layer, expert))
-    pool = ExpertPool(spec.layout, slots, layers=layers, experts=spec.experts, device=device)
-    pooled = [assemble.build_layer(spec, SEED, device, layer=l, pool=pool, host_store=store) for l in range(layers)]
-    dense = [assemble.build_layer(spec, SEED, device, layer=l, dense=True) for l in range(layers)]
-    return store, pool, pooled, dense
+    return pooled_stack(device, spec, layers, slots, SEED)
 
 
 def _expected_table(ref, layers, experts):
@@ -137,3 +130,63 @@ def test_full_size_records_through_the_device_lru(device):
     np.testing.assert_array_equal(lru.state()[0], _expected_table(ref, layers, FULL.experts))
     assert lru.stats()["misses"] == ref.misses > slots
     _check_records(pool, store, ref)
+
+
+def test_device_lru_queue_longer_than_one_block(device):
+    """1100 slots: every thread of the assign block holds a run of two queue
+    entries.  The pool is warmed by the host LRU (all 1280 keys in a shuffled
+    order, so the queue starts with evictions behind it), then the device
+    continues; its queue must equal the reference's free list + OrderedDict."""
+    import random
+
+    layers, slots = 20, 1100
+    store, pool, pooled, dense = _setup(device, SMALL, layers, slots)
+    ref = pool_oracle.LruSlots(slots)
+    rnd = random.Random(3)
+    for layer in rnd.sample(range(layers), layers):
+        experts = rnd.sample(range(SMALL.experts), SMALL.experts)
+        _, misses = pool.assign(layer, experts)
+        assert misses == ref.assign(layer, experts)[1]
+        pool.fill(layer, misses, store)
+    host_hits, host_misses = ref.hits, ref.misses
+    lru = pool.attach_device_lru(store)
+    assert lru.order_len == slots
+    for step in range(40):
+        layer = rnd.randrange(layers)
+        routed = _step(SMALL, pooled, dense, layer, 1 + step % 8, 600 + step, device)
+        ref.assign(layer, routed)
+        if step % 10 == 9:
+            table, owner, order = lru.state()
+            np.testing.assert_array_equal(table, _expected_table(ref, layers, SMALL.experts), err_msg=f"step {step}")
+            assert order.tolist() == list(reversed(ref.free)) + list(ref.slot_of.values()), step
+    stats = lru.stats()
+    assert (stats["hits"], stats["misses"]) == (ref.hits - host_hits, ref.misses - host_misses)
+    _check_records(pool, store, ref)
+
+
+def test_a_queue_with_a_foreign_slot_leaves_the_state_untouched(device):
+    """An entry outside 0..slots-1 in the queue: the call sets status bit 16,
+    maps and fills nothing, and leaves table, owners, queue and counters as
+    they were (the layer's experts then see unmapped slots: status bit 1)."""
+    from veymoe import _lib
+    from veymoe.device import stream_handle
+
+    layers, slots = 1, 40
+    store, pool, pooled, dense = _setup(device, SMALL, layers, slots)
+    lru = pool.attach_device_lru(store)
+    _step(SMALL, pooled, dense, 0, 2, 700, device)          # a valid call first
+    lru.lru_order[5] = slots + 3
+    before = [t.clone() for t in (pool.slot_table, lru.slot_owner, lru.lru_order, lru.counters)]
+    layer = pooled[0]
+    x = assemble.tokens_tensor(SMALL, SEED, device, 3, stream=701)
+    out = torch.empty_like(x)
+    inds = torch.empty((3, layer.top_k), dtype=torch.int32, device=device)
+    scores = torch.empty((3, layer.top_k), dtype=x.dtype, device=device)
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    a = layer.layer_args(x, out, inds, scores)
+    a.status = status.data_ptr()
+    _lib.check(_lib.lib().vm_moe_layer_lru(a, lru.view(0), stream_handle()))
+    torch.cuda.synchronize()
+    assert int(status.item()) & 16
+    for b, t in zip(before, (pool.slot_table, lru.slot_owner, lru.lru_order, lru.counters)):
+        assert torch.equal(b, t)

@@ -612,7 +612,7 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   if (T == 0 || T > VM_LAYER_MAX_TOKENS)
     return fail(VM_EUNSUPPORTED, "the device LRU serves decode calls of 1..%d tokens", VM_LAYER_MAX_TOKENS);
   if (a->phases != 0) return fail(VM_EINVAL, "vm_moe_layer_lru runs the whole layer (phases must be 0)");
-  if (lru->slot_table == nullptr || lru->slot_owner == nullptr || lru->slot_stamp == nullptr ||
+  if (lru->slot_table == nullptr || lru->slot_owner == nullptr || lru->lru_order == nullptr ||
       lru->counters == nullptr || lru->host_row == nullptr || lru->host_store == nullptr)
     return fail(VM_EINVAL, "device LRU state pointers are required");
   if (a->pool.base == nullptr) return fail(VM_EINVAL, "the device LRU needs a pool view");
@@ -621,8 +621,10 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
     return fail(VM_EINVAL, "LRU slots (%u) must equal the pool records (%u)", lru->slots, a->pool.records);
   if (lru->slots > vm::kLruMaxSlots)
     return fail(VM_EUNSUPPORTED, "the device LRU holds at most %u slots", vm::kLruMaxSlots);
-  if (uint64_t(T) * K > lru->slots || uint64_t(T) * K > vm::kLruMaxRouted)
-    return fail(VM_EINVAL, "tokens * top_k = %u exceeds the pool or the %u routed ids of one call", T * K,
+  if (lru->order_len > lru->slots)
+    return fail(VM_EINVAL, "order_len (%u) exceeds the slots (%u)", lru->order_len, lru->slots);
+  if (uint64_t(T) * K > lru->order_len || uint64_t(T) * K > vm::kLruMaxRouted)
+    return fail(VM_EINVAL, "tokens * top_k = %u exceeds the queued slots or the %u routed ids of one call", T * K,
                 vm::kLruMaxRouted);
   if (uint64_t(lru->layers) * E > 0x7fffffffull) return fail(VM_EINVAL, "layers * expert_count is too large");
   VmLayerArgs r = *a;
@@ -661,7 +663,7 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   vm::LruLaunch l{};
   l.slot_table = lru->slot_table;
   l.slot_owner = lru->slot_owner;
-  l.slot_stamp = lru->slot_stamp;
+  l.lru_order = lru->lru_order;
   l.counters = lru->counters;
   l.host_row = lru->host_row;
   l.fill_count = fill;
@@ -674,6 +676,7 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   l.layers = lru->layers;
   l.layer = lru->layer;
   l.slots = lru->slots;
+  l.order_len = lru->order_len;
   e = vm::launch_select_lru(sel, l, stream);
   if (e != hipSuccess) return hip_fail(e, "select/lru launch");
   vm::FillLaunch f{};

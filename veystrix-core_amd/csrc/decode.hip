@@ -422,6 +422,8 @@ __global__ __launch_bounds__(64) void k_select_f32(SelectLaunch p) { select_body
 // (softmax, top-k, renormalised scores, as select_body), then the block
 // applies the LRU assign to the routed ids, tokens in order and slots in rank
 // order (vm_lru.h).
+static_assert(64 * kMaxExpertsPerLane <= kLruMaxExperts, "routed ids must fit the LRU's LDS map");
+
 template <class A>
 __global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruLaunch l) {
   __shared__ typename Cand<A>::T s_cands[kLruWaves][kMaxCand];
@@ -429,6 +431,8 @@ __global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruL
   __shared__ LruShared sh;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
+  LruRegs r;
+  lru_begin(l, sh, r);  // independent of the routing: in flight during the selection
   if (wave < p.tokens) {
     const uint32_t t = wave;
     GateKeys<A> g;
@@ -445,8 +449,9 @@ __global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruL
       s_routed[o] = static_cast<int32_t>(e);
     }
   }
-  __syncthreads();
-  lru_assign(l, s_routed, sh);
+  lru_owners(l, r);
+  lds_barrier();
+  lru_assign(l, s_routed, sh, r);
 }
 
 // -------------------------------------------------------------- front -----

@@ -164,30 +164,6 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
   return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
-// One step of a 64-bit unsigned min through DPP: lanes without a source keep
-// their own value (old = own), so the min leaves them unchanged.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ uint64_t dpp_min_u64(uint64_t v) {
-  const int lo = static_cast<int>(static_cast<uint32_t>(v)), hi = static_cast<int>(static_cast<uint32_t>(v >> 32));
-  const uint32_t olo = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(lo, lo, CTRL, ROW_MASK, 0xF, false));
-  const uint32_t ohi = static_cast<uint32_t>(__builtin_amdgcn_update_dpp(hi, hi, CTRL, ROW_MASK, 0xF, false));
-  const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;
-  return o < v ? o : v;
-}
-
-// Wave-wide 64-bit unsigned min, broadcast to every lane.
-__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-  v = dpp_min_u64<kDppQuadXor1>(v);
-  v = dpp_min_u64<kDppQuadXor2>(v);
-  v = dpp_min_u64<kDppHalfMirror>(v);
-  v = dpp_min_u64<kDppMirror>(v);
-  v = dpp_min_u64<kDppBcast15, 0xA>(v);
-  v = dpp_min_u64<kDppBcast31, 0xC>(v);
-  const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v)), 63));
-  const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(static_cast<uint32_t>(v >> 32)), 63));
-  return (static_cast<uint64_t>(hi) << 32) | lo;
-}
-
 __device__ __forceinline__ uint64_t readlane_u64(uint64_t v, uint32_t lane) {
   const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
   const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v >> 32), lane));

@@ -84,7 +84,7 @@ struct DownLaunch {
 // ------------------------------------------------------ device-side LRU --
 constexpr uint32_t kLruMaxRouted = 80;  // VM_LAYER_MAX_TOKENS * MAX_TOP_K
 constexpr int kLruThreads = 1024;       // one block runs the selection and the assign
-constexpr int kLruSlotsPerThread = 32;  // slot stamps each thread holds in registers
+constexpr int kLruSlotsPerThread = 32;  // queue entries each thread holds in registers
 constexpr uint32_t kLruMaxSlots = kLruThreads * kLruSlotsPerThread;
 constexpr uint32_t kNoRecord = 0xffffffffu;
 
@@ -92,7 +92,7 @@ constexpr uint32_t kNoRecord = 0xffffffffu;
 struct LruLaunch {
   int32_t* slot_table;         // [layers, experts]
   int32_t* slot_owner;         // [slots]
-  uint64_t* slot_stamp;        // [slots]
+  int32_t* lru_order;          // [order_len] slot ids, least recently used first
   uint64_t* counters;          // [4 + 4 * layers]
   const int32_t* host_row;     // [layers, experts]
   uint32_t* fill_count;        // [1] misses of the call
@@ -100,7 +100,7 @@ struct LruLaunch {
   uint32_t* fill_dst;          // [routed] slot of miss m
   uint32_t* status;
   uint64_t host_records;
-  uint32_t routed, experts, layers, layer, slots;
+  uint32_t routed, experts, layers, layer, slots, order_len;
 };
 
 // Copy of the missed records from pinned host memory into their slots.

@@ -117,7 +117,7 @@ class VmDeviceLru(ctypes.Structure):
     _fields_ = [
         ("slot_table", _vp),
         ("slot_owner", _vp),
-        ("slot_stamp", _vp),
+        ("lru_order", _vp),
         ("counters", _vp),
         ("host_row", _vp),
         ("host_store", _vp),
@@ -126,7 +126,7 @@ class VmDeviceLru(ctypes.Structure):
         ("layers", _c_u32),
         ("layer", _c_u32),
         ("slots", _c_u32),
-        ("reserved", _c_u32),
+        ("order_len", _c_u32),
     ]
 
 

@@ -21,8 +21,9 @@ Counterpart of the reference's ``ExpertPool`` (models/flashnext/expert_pool.py:7
 * ``attach_device_lru`` moves the LRU state to the device (``DeviceLru``):
   decode layers then assign, fill and run with ``vm_moe_layer_lru`` without
   any route sync to the host (the reference syncs every layer,
-  expert_cache.py:1738-1749).  Recency there is one distinct stamp per slot,
-  converted from and back to this class's OrderedDict order exactly.
+  expert_cache.py:1738-1749).  Recency there is one queue of slot ids (the
+  free list in pop order, then the OrderedDict's slots), converted from and
+  back to this class's state exactly.
 """
 from __future__ import annotations
 
@@ -307,8 +308,8 @@ class ExpertPool:
         lru = self.device_lru
         if lru is None:
             return
-        table, owner, stamp = lru.state()
-        restore_from_stamps(self, owner, stamp)
+        table, owner, order = lru.state()
+        restore_from_order(self, owner, order)
         if not np.array_equal(table, self._host_table):
             raise RuntimeError("device slot table disagrees with the slot owners")
         stats = lru.stats()
@@ -318,47 +319,42 @@ class ExpertPool:
         self.device_lru = None
 
 
-def stamp_state(pool: ExpertPool):
-    """The pool's LRU order as one distinct stamp per slot, the form the device
-    LRU keeps: free slots get 1..n in the order the free list pops them (from
-    its end), then resident keys n+1.. from least to most recently used.
-    Slots that are neither free nor resident keep stamp 0 (never chosen).
-    Returns (owner [slots] int32 = layer * experts + expert or -1,
-    stamp [slots] uint64, last stamp issued)."""
+def order_state(pool: ExpertPool):
+    """The pool's LRU state in the form the device LRU keeps: one queue of
+    slot ids, least recently used first, which is the free list in the order
+    it pops (from its end) followed by the resident slots from least to most
+    recently used (the OrderedDict order).  Slots that are neither free nor
+    resident are not queued and never handed out.  Returns (owner [slots]
+    int32 = layer * experts + expert or -1, order [usable_slots] int32)."""
     owner = np.full(pool.slots, -1, dtype=np.int32)
-    stamp = np.zeros(pool.slots, dtype=np.uint64)
-    free = pool._free
-    n = len(free)
-    for i, slot in enumerate(free):
-        stamp[slot] = n - i
-    for j, ((layer, expert), slot) in enumerate(pool._slot_of.items()):
+    for (layer, expert), slot in pool._slot_of.items():
         owner[slot] = layer * pool.experts + expert
-        stamp[slot] = n + 1 + j
-    return owner, stamp, n + len(pool._slot_of)
+    order = np.array(list(reversed(pool._free)) + list(pool._slot_of.values()), dtype=np.int32)
+    return owner, order
 
 
-def restore_from_stamps(pool: ExpertPool, owner: np.ndarray, stamp: np.ndarray) -> None:
-    """Inverse of ``stamp_state``: rebuild the free list, the OrderedDict and
-    the host slot table of ``pool`` from per-slot owners and stamps."""
+def restore_from_order(pool: ExpertPool, owner: np.ndarray, order: np.ndarray) -> None:
+    """Inverse of ``order_state``: rebuild the free list, the OrderedDict and
+    the host slot table of ``pool`` from per-slot owners and the queue."""
     owner = np.asarray(owner)
-    stamp = np.asarray(stamp, dtype=np.uint64)
-    slots = np.arange(pool.slots)
-    free = slots[(owner < 0) & (stamp > 0)]
-    resident = slots[owner >= 0]
-    pool._free = [int(s) for s in free[np.argsort(stamp[free], kind="stable")[::-1]]]
+    order = [int(s) for s in np.asarray(order)]
+    if len(set(order)) != len(order) or any(not 0 <= s < pool.slots for s in order):
+        raise RuntimeError("the LRU queue does not list distinct slots of the pool")
+    pool._free = [s for s in reversed(order) if owner[s] < 0]
     pool._slot_of = OrderedDict()
     pool._host_table[:] = -1
-    for slot in resident[np.argsort(stamp[resident], kind="stable")]:
-        layer, expert = divmod(int(owner[slot]), pool.experts)
-        pool._slot_of[(layer, expert)] = int(slot)
-        pool._host_table[layer, expert] = int(slot)
+    for slot in order:
+        if owner[slot] >= 0:
+            layer, expert = divmod(int(owner[slot]), pool.experts)
+            pool._slot_of[(layer, expert)] = slot
+            pool._host_table[layer, expert] = slot
     pool._dirty.clear()
 
 
 class DeviceLru:
     """The LRU state of an ``ExpertPool`` on the device (``VmDeviceLru``):
-    the slot table (the pool's own device table), per-slot owners and stamps,
-    counters, and the host-store row of every (layer, expert)."""
+    the slot table (the pool's own device table), per-slot owners, the LRU
+    queue, counters, and the host-store row of every (layer, expert)."""
 
     def __init__(self, pool: ExpertPool, source: HostRecordStore):
         if source.layout.record_bytes != pool.layout.record_bytes:
@@ -366,15 +362,15 @@ class DeviceLru:
         if not source.buffer.is_pinned():
             raise ValueError("the host store must be pinned memory")
         pool.sync_tables()
-        owner, stamp, last = stamp_state(pool)
+        owner, order = order_state(pool)
         dev = pool.device
         self.pool = pool
         self.store = source
         self.usable_slots = pool.usable_slots
         self.slot_owner = torch.from_numpy(owner).to(dev)
-        self.slot_stamp = torch.from_numpy(stamp.view(np.int64)).to(dev)
+        self.order_len = len(order)
+        self.lru_order = torch.from_numpy(order).to(dev)
         counters = np.zeros(4 + 4 * pool.layers, dtype=np.int64)
-        counters[0] = last
         self.counters = torch.from_numpy(counters).to(dev)
         host_row = np.full((pool.layers, pool.experts), -1, dtype=np.int32)
         for (layer, expert), row in source._row_of.items():
@@ -389,7 +385,7 @@ class DeviceLru:
             v = _lib.VmDeviceLru()
             v.slot_table = self.pool.slot_table.data_ptr()
             v.slot_owner = self.slot_owner.data_ptr()
-            v.slot_stamp = self.slot_stamp.data_ptr()
+            v.lru_order = self.lru_order.data_ptr()
             v.counters = self.counters.data_ptr()
             v.host_row = self.host_row.data_ptr()
             v.host_store = self.store.buffer.data_ptr()
@@ -398,6 +394,7 @@ class DeviceLru:
             v.layers = self.pool.layers
             v.layer = int(layer)
             v.slots = self.pool.slots
+            v.order_len = self.order_len
             self._views[layer] = v
         return v
 
@@ -405,14 +402,13 @@ class DeviceLru:
         """Counters (synchronizes): pool-wide, or of one layer."""
         c = self.counters.cpu().numpy()
         if layer is None:
-            return {"last_stamp": int(c[0]), "hits": int(c[1]), "misses": int(c[2]), "routed_hits": int(c[3])}
+            return {"assigned": int(c[0]), "hits": int(c[1]), "misses": int(c[2]), "routed_hits": int(c[3])}
         r = c[4 + 4 * layer: 8 + 4 * layer]
         return {"hits": int(r[0]), "misses": int(r[1]), "routed_hits": int(r[2]), "routed": int(r[3])}
 
     def state(self):
-        """(slot table [layers, experts], owners [slots], stamps [slots]) on the host."""
-        return (self.pool.slot_table.cpu().numpy(), self.slot_owner.cpu().numpy(),
-                self.slot_stamp.cpu().numpy().view(np.uint64))
+        """(slot table [layers, experts], owners [slots], LRU queue [order_len]) on the host."""
+        return (self.pool.slot_table.cpu().numpy(), self.slot_owner.cpu().numpy(), self.lru_order.cpu().numpy())
 
 
 def route_words(slots_of: dict, routed) -> np.ndarray:
@@ -420,5 +416,5 @@ def route_words(slots_of: dict, routed) -> np.ndarray:
     return np.array([SLOT_BIT | slots_of[int(e)] for e in routed], dtype=np.uint32)
 
 
-__all__ = ["DeviceLru", "ExpertPool", "HostRecordStore", "PARTS", "SLOT_BIT", "restore_from_stamps",
-           "route_words", "stamp_state"]
+__all__ = ["DeviceLru", "ExpertPool", "HostRecordStore", "PARTS", "SLOT_BIT", "order_state", "restore_from_order",
+           "route_words"]
