@@ -10,8 +10,9 @@
 //            rows are all the tokens.
 //   gemm     one workgroup per (tile of <= 64 rows of one group, slice of output
 //            features).  Workgroups are dealt to the eight XCDs round-robin;
-//            the slices of one row tile take blocks of the same XCD so that
-//            they share its L2 copy of the tile's A rows.  K runs in chunks of
+//            each XCD takes a contiguous run of the sorted tiles with all their
+//            slices, so the slices of one row tile share its L2 copy of the
+//            tile's A rows and the tiles of one expert share its weights.  K runs in chunks of
 //            eight 32-input groups.  Per chunk the block stages in LDS (double
 //            buffered): the A rows (32 lanes per 512-byte row segment,
 //            pair-permuted to match the dequantised weights), the Q4 weight
@@ -494,6 +495,12 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #ifndef VM_DN_WAVES_PER_EU
 #define VM_DN_WAVES_PER_EU 2
 #endif
+// Block order of sorted tiles: 0 deals row tiles to the XCDs round-robin
+// (tile t on XCD t % 8); 1 gives each XCD a contiguous run of the tiles, so
+// the row tiles of one expert share that XCD's L2 copy of its weights.
+#ifndef VM_G_MAP
+#define VM_G_MAP 1
+#endif
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(EPI == kEpiRows ? VM_DN_WAVES_PER_EU : VM_G_WAVES_PER_EU)))
@@ -509,12 +516,22 @@ void k_grouped(GroupedLaunch p) {
   // XCD-aware order: workgroups are dealt to the eight XCDs round-robin, so
   // block L runs on XCD L % 8.  The column slices of one row tile take
   // consecutive blocks of the same XCD and share its L2 copy of the tile's A
-  // rows; eight row tiles run side by side, one per XCD.  The grid is
-  // slices * (tile bound rounded up to a multiple of 8).
+  // rows.  Sorted tiles: XCD x takes the x-th eighth of the tiles in order,
+  // so the row tiles of one expert also follow each other on one XCD and
+  // share its weights.  The grid is slices * (tile bound rounded up to a
+  // multiple of 8); blocks past the live tile count exit.
   const uint32_t slices = (p.n_dim + WAVES * NBW * 16 - 1) / (WAVES * NBW * 16);
   const uint32_t lin = blockIdx.x, r8 = lin >> 3;
-  const uint32_t slice = r8 % slices;
-  const uint32_t tile = (r8 / slices) * 8 + (lin & 7u);
+  uint32_t slice = r8 % slices;
+  uint32_t tile = (r8 / slices) * 8 + (lin & 7u);
+#if VM_G_MAP == 1
+  if (p.tiles != nullptr) {
+    const uint32_t chunk = (*p.tile_count + 7u) / 8u;
+    const uint32_t local = r8 / slices;
+    if (local >= chunk) return;
+    tile = (lin & 7u) * chunk + local;
+  }
+#endif
 
   // the tile: rows [row0, row0 + rows) of `group`
   uint32_t group = 0, row0, rows;
