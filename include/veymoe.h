@@ -27,6 +27,9 @@
  *   vm_moe_layer_lru   _pool_pass (route sync, assign, fill, execute)
  *                                                       models/flashnext/expert_cache.py:1709-1772,1842-1947
  *                                                       models/flashnext/expert_pool.py:123-159,201-220
+ *   vm_hyper_mix       the branch's hyper-connection    models/flashnext/qwen4_verifier.py:20-33
+ *                      (hc_norm RMSNorm)                models/flashnext/patch_rmsnorm.py:108-135
+ *   VmLayerArgs.inject_*  _inject after the branch      models/flashnext/compile_glue.py:32-41
  *   vm_available       flashnext_native_available       metal_runtime_native.mm:196-201
  *   vm_last_error      flashnext_native_get_last_error  metal_runtime_native.mm:203-209
  */
@@ -40,7 +43,7 @@
 extern "C" {
 #endif
 
-#define VM_ABI_VERSION 1
+#define VM_ABI_VERSION 2
 
 /* status codes (0 = ok) */
 #define VM_OK 0
@@ -196,9 +199,53 @@ typedef struct VmLayerArgs {
                       inds/scores (inds_out/scores_out or the workspace) for a
                       later experts-only call with the same workspace, so the
                       host can resolve pool misses in between. */
+  /* Optional hyper-connection injection of the layer output y into the
+   * residual streams, in the experts' final epilogue (replaces the decoder's
+   * _inject, compile_glue.py:32-35):
+   *   inject_out[t, j*H + h] = round(inject_hidden[t, j*H + h]
+   *                                  + round(y[t, h] * inject_weights[t, j]))
+   * for j < hc_count (1..VM_MAX_STREAMS), activation dtype; `output` still
+   * receives y.  inject_out may equal inject_hidden.  NULL inject_out: off. */
+  const void* inject_hidden;     /* [tokens, hc_count * hidden] */
+  const void* inject_weights;    /* [tokens, hc_count] */
+  void* inject_out;              /* [tokens, hc_count * hidden] */
+  uint32_t hc_count;
+  uint32_t reserved;
 } VmLayerArgs;
 #define VM_PHASE_ROUTER 1u
 #define VM_PHASE_EXPERTS 2u
+#define VM_MAX_STREAMS 8
+
+/* vm_hyper_mix: the hyper-connection in front of a decoder branch, for any
+ * token count (qwen4_verifier.py:20-33, Qwen4ExpGatedResidual; the norm is
+ * patch_rmsnorm.py:108-135).  With n = hc_count * hidden_size:
+ *   normed  = rms_norm(hidden)            fp32 mean of squares over the whole
+ *             row (norm_group 0) or groups of norm_group; gain = weight
+ *             (one_centered) or 1 + weight
+ *   d       = silu(mix_down . normed / hc_count)          [lowrank]
+ *   mixed   = mean_j(sigmoid(mix_up . d)_j * normed_j)    [hidden], the branch input
+ *   weights = 2 * sigmoid(inject . normed / hc_count)     [hc_count]
+ * Q4/G32 projections in the vector form, every step rounded to the
+ * activation dtype.  Requirements: n % 64 == 0, n <= 16384, norm_group 0 or
+ * a multiple of 64 dividing n, lowrank a multiple of 32 up to 256,
+ * hc_count 1..VM_MAX_STREAMS, 16-byte aligned hidden rows.  The workspace
+ * (vm_hyper_mix_workspace bytes) receives normed and d unless `normed` is
+ * given. */
+typedef struct VmHyperArgs {
+  const void* hidden;            /* [tokens, n] the residual streams */
+  const void* norm_weight;       /* [n] hc_norm gain, activation dtype */
+  VmQ4Proj mix_down;             /* [lowrank, n/8] */
+  VmQ4Proj mix_up;               /* [n, lowrank/8] */
+  VmQ4Proj inject;               /* [hc_count, n/8] */
+  void* mixed;                   /* out [tokens, hidden] */
+  void* weights;                 /* out [tokens, hc_count] */
+  void* normed;                  /* optional out [tokens, n] */
+  void* workspace;
+  uint64_t workspace_bytes;
+  uint32_t tokens, hidden_size, hc_count, lowrank, norm_group, one_centered;
+  uint32_t act_dtype;
+  float eps;
+} VmHyperArgs;
 
 /* vm_moe_layer_lru: the decode layer (tokens <= VM_LAYER_MAX_TOKENS) over an
  * expert pool whose LRU state lives on the device, so the call never waits for
@@ -303,6 +350,11 @@ uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden
 int vm_moe_layer(const VmLayerArgs* args, void* stream);
 /* Workspace: vm_moe_layer_workspace() of the same shape. */
 int vm_moe_layer_lru(const VmLayerArgs* args, const VmDeviceLru* lru, void* stream);
+
+/* The hyper-connection before a branch (see VmHyperArgs): two launches. */
+uint64_t vm_hyper_mix_workspace(uint32_t tokens, uint32_t hc_count, uint32_t hidden_size, uint32_t lowrank,
+                                uint32_t act_dtype);
+int vm_hyper_mix(const VmHyperArgs* args, void* stream);
 
 uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size,
                                   uint32_t inter_size, uint32_t expert_count, uint32_t act_dtype);

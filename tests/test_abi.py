@@ -26,14 +26,14 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
-    assert lib.vm_abi_version() == 1
+    assert lib.vm_abi_version() == 2
 
 
 def test_struct_layouts_match_the_header(tmp_path):
     structs = {
         "VmQ4Proj": _lib.VmQ4Proj, "VmPoolView": _lib.VmPoolView, "VmMoeArgs": _lib.VmMoeArgs,
         "VmRouterArgs": _lib.VmRouterArgs, "VmLayerArgs": _lib.VmLayerArgs, "VmGroupedArgs": _lib.VmGroupedArgs,
-        "VmDeviceLru": _lib.VmDeviceLru,
+        "VmDeviceLru": _lib.VmDeviceLru, "VmHyperArgs": _lib.VmHyperArgs,
     }
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for name, cls in structs.items():
@@ -152,3 +152,56 @@ def test_library_has_no_cpu_fallback_symbols():
     out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
     assert {n for n in exported if n.startswith("vm_")} == set(_declared())
+
+
+def _hyper_call(**kw):
+    """vm_hyper_mix on fake pointers: every case must fail validation."""
+    a = _lib.VmHyperArgs()
+    a.hidden, a.norm_weight, a.mixed, a.weights, a.workspace = 256, 512, 768, 1024, 4096
+    for proj, base in (("mix_down", 8192), ("mix_up", 16384), ("inject", 24576)):
+        q = getattr(a, proj)
+        q.weight, q.scales, q.biases = base, base + 2048, base + 4096
+    a.tokens, a.hidden_size, a.hc_count, a.lowrank, a.norm_group, a.one_centered = 1, 256, 4, 32, 0, 1
+    a.workspace_bytes = 1 << 20
+    a.eps = 1e-6
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return _lib.lib().vm_hyper_mix(ctypes.byref(a), None)
+
+
+@pytest.mark.parametrize("field,value,code,message", [
+    ("hc_count", 0, _lib.VM_EINVAL, "hc_count"),
+    ("hc_count", 9, _lib.VM_EINVAL, "hc_count"),
+    ("hidden_size", 4100, _lib.VM_EUNSUPPORTED, "multiple of 64"),
+    ("lowrank", 48, _lib.VM_EUNSUPPORTED, "lowrank"),
+    ("norm_group", 96, _lib.VM_EUNSUPPORTED, "norm_group"),
+    ("mixed", None, _lib.VM_EINVAL, "required"),
+    ("hidden", 258, _lib.VM_EINVAL, "aligned"),
+    ("workspace_bytes", 16, _lib.VM_EWORKSPACE, "workspace"),
+    ("tokens", 70000, _lib.VM_EUNSUPPORTED, "65535"),
+])
+def test_hyper_mix_rejects_bad_arguments_without_a_device(field, value, code, message):
+    assert _hyper_call(**{field: value}) == code
+    assert message in _lib.last_error()
+
+
+def test_hyper_mix_workspace_size():
+    lib = _lib.lib()
+    # normed [T, n] bf16 then d [T, lowrank] bf16, each 256-byte aligned
+    assert lib.vm_hyper_mix_workspace(1, 4, 2048, 32, 0) == 8192 * 2 + 256
+    assert lib.vm_hyper_mix_workspace(3, 4, 2048, 32, 1) == 3 * 8192 * 4 + 512
+
+
+def test_layer_injection_is_validated_without_a_device():
+    a = _lib.VmLayerArgs()
+    a.x, a.output, a.router_weight = 256, 512, 768
+    a.tokens, a.hidden_size, a.inter_size, a.expert_count, a.top_k, a.group_size = 1, 64, 64, 8, 2, 32
+    a.gate.weight = a.up.weight = a.down.weight = 4096
+    a.gate.scales = a.up.scales = a.down.scales = 8192
+    a.gate.biases = a.up.biases = a.down.biases = 8192
+    a.inject_out = 16384
+    assert _lib.lib().vm_moe_layer(ctypes.byref(a), None) == _lib.VM_EINVAL
+    assert "inject_hidden" in _lib.last_error()
+    a.inject_hidden, a.inject_weights, a.hc_count = 16384, 20480, 9
+    assert _lib.lib().vm_moe_layer(ctypes.byref(a), None) == _lib.VM_EINVAL
+    assert "hc_count" in _lib.last_error()

@@ -444,7 +444,26 @@ static int validate_layer(const VmLayerArgs* a) {
   if (rc != VM_OK) return rc;
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  if (a->inject_out != nullptr) {
+    if (a->inject_hidden == nullptr || a->inject_weights == nullptr)
+      return fail(VM_EINVAL, "an injection needs inject_hidden and inject_weights");
+    if (a->hc_count == 0 || a->hc_count > VM_MAX_STREAMS)
+      return fail(VM_EINVAL, "hc_count must be 1..%d", VM_MAX_STREAMS);
+    if (!aligned16(a->inject_hidden) || !aligned16(a->inject_out))
+      return fail(VM_EINVAL, "inject_hidden and inject_out must be 16-byte aligned");
+  }
   return VM_OK;
+}
+
+static vm::Inject to_inject(const VmLayerArgs* a) {
+  vm::Inject j{};
+  if (a->inject_out != nullptr) {
+    j.hidden = a->inject_hidden;
+    j.weights = a->inject_weights;
+    j.out = a->inject_out;
+    j.hc = a->hc_count;
+  }
+  return j;
 }
 
 int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
@@ -465,6 +484,12 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
     c.output = static_cast<float*>(a->output) + uint64_t(t0) * H;
     if (a->inds_out != nullptr) c.inds_out = a->inds_out + uint64_t(t0) * K;
     if (a->scores_out != nullptr) c.scores_out = static_cast<float*>(a->scores_out) + uint64_t(t0) * K;
+    if (a->inject_out != nullptr) {
+      const uint64_t streams = uint64_t(t0) * a->hc_count;
+      c.inject_hidden = static_cast<const float*>(a->inject_hidden) + streams * H;
+      c.inject_weights = static_cast<const float*>(a->inject_weights) + streams;
+      c.inject_out = static_cast<float*>(a->inject_out) + streams * H;
+    }
     rc = layer_decode(&c, stream);
     if (rc != VM_OK) return rc;
   }
@@ -565,6 +590,7 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   d.scores = scores;
   d.score_dtype = static_cast<int>(a->act_dtype);
   d.out = a->output;
+  d.inject = to_inject(a);
   d.status = a->status;
   d.tokens = T;
   d.slots = K;
@@ -602,6 +628,68 @@ static int host_device_pointer(const void* host, const uint8_t** out) {
     last_dev = static_cast<const uint8_t*>(dev);
   }
   *out = last_dev;
+  return VM_OK;
+}
+
+// Workspace of vm_hyper_mix: normed [T, n] then d [T, lowrank], activation dtype.
+static uint64_t hyper_normed_bytes(uint32_t tokens, uint32_t n, uint32_t act_dtype) {
+  return align_up(uint64_t(tokens) * n * (act_dtype == VM_F32 ? 4 : 2));
+}
+
+uint64_t vm_hyper_mix_workspace(uint32_t tokens, uint32_t hc_count, uint32_t hidden_size, uint32_t lowrank,
+                                uint32_t act_dtype) {
+  const uint32_t n = hc_count * hidden_size;
+  return hyper_normed_bytes(tokens, n, act_dtype) + align_up(uint64_t(tokens) * lowrank * (act_dtype == VM_F32 ? 4 : 2));
+}
+
+int vm_hyper_mix(const VmHyperArgs* a, void* stream_ptr) {
+  if (a == nullptr) return fail(VM_EINVAL, "null arguments");
+  const uint32_t T = a->tokens, H = a->hidden_size, hc = a->hc_count, r = a->lowrank;
+  if (T == 0 || H == 0) return fail(VM_EINVAL, "tokens and hidden_size must be positive");
+  if (T > 65535) return fail(VM_EUNSUPPORTED, "at most 65535 tokens per call");
+  if (hc == 0 || hc > VM_MAX_STREAMS) return fail(VM_EINVAL, "hc_count must be 1..%d", VM_MAX_STREAMS);
+  if (a->act_dtype != VM_BF16 && a->act_dtype != VM_F32) return fail(VM_EINVAL, "act_dtype must be bf16 or f32");
+  const uint64_t n64 = uint64_t(hc) * H;
+  if (n64 % 64 || n64 > vm::kHcMaxRow)
+    return fail(VM_EUNSUPPORTED, "hc_count * hidden_size must be a multiple of 64 up to %u", vm::kHcMaxRow);
+  const uint32_t n = static_cast<uint32_t>(n64);
+  if (r == 0 || r % 32 || r > vm::kHcMaxLowrank)
+    return fail(VM_EUNSUPPORTED, "lowrank must be a multiple of 32 up to %u", vm::kHcMaxLowrank);
+  const uint32_t gs = a->norm_group == 0 ? n : a->norm_group;
+  if (gs % 64 || n % gs) return fail(VM_EUNSUPPORTED, "norm_group must be 0 or a multiple of 64 dividing the row");
+  if (a->hidden == nullptr || a->norm_weight == nullptr || a->mixed == nullptr || a->weights == nullptr)
+    return fail(VM_EINVAL, "hidden, norm_weight, mixed and weights are required");
+  if (!aligned16(a->hidden)) return fail(VM_EINVAL, "hidden must be 16-byte aligned");
+  if (a->mix_down.weight == nullptr || a->mix_up.weight == nullptr || a->inject.weight == nullptr ||
+      !proj_ok(a->mix_down) || !proj_ok(a->mix_up) || !proj_ok(a->inject))
+    return fail(VM_EINVAL, "mix_down, mix_up and inject projections are required");
+  if (!aligned16(a->mix_down.weight) || !aligned16(a->mix_up.weight) || !aligned16(a->inject.weight))
+    return fail(VM_EINVAL, "projection weights must be 16-byte aligned");
+  const uint64_t need = vm_hyper_mix_workspace(T, hc, H, r, a->act_dtype);
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)need);
+  char* ws = static_cast<char*>(a->workspace);
+  vm::HcLaunch p{};
+  p.hidden = a->hidden;
+  p.norm_weight = a->norm_weight;
+  p.down = to_ptrs(a->mix_down);
+  p.up = to_ptrs(a->mix_up);
+  p.inj = to_ptrs(a->inject);
+  p.normed = a->normed != nullptr ? a->normed : ws;
+  p.d = ws + hyper_normed_bytes(T, n, a->act_dtype);
+  p.mixed = a->mixed;
+  p.weights = a->weights;
+  p.eps = a->eps;
+  p.tokens = T;
+  p.width = H;
+  p.hc = hc;
+  p.n = n;
+  p.lowrank = r;
+  p.norm_group = gs;
+  p.one_centered = a->one_centered ? 1u : 0u;
+  p.act_dtype = static_cast<int>(a->act_dtype);
+  const hipError_t e = vm::launch_hyper_mix(p, static_cast<hipStream_t>(stream_ptr));
+  if (e != hipSuccess) return hip_fail(e, "hyper-connection launch");
   return VM_OK;
 }
 
@@ -714,6 +802,7 @@ struct GroupedExperts {
   const void* sig;
   const void* shared_y;
   void* output;
+  vm::Inject inject;
   uint32_t* status;
   uint32_t T, K, H, I, E;
   int mode;
@@ -792,6 +881,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   }
   c.shared_y = g.shared_y;
   c.out = g.output;
+  c.inject = g.inject;
   c.tokens = g.T;
   c.slots = g.K;
   c.hidden = g.H;
@@ -879,6 +969,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   g.shared_down = a->shared_down_proj;
   g.sig = sig;
   g.output = a->output;
+  g.inject = to_inject(a);
   g.status = a->status;
   g.T = T;
   g.K = K;

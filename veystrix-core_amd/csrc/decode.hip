@@ -859,6 +859,16 @@ __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
   }
   if (take_shared) r_shared = A::load_bits(sh_src, static_cast<size_t>(t) * H + row0 + er);
   if (take_sig) r_sig = A::load_bits(sig_src, t);
+  // the streams this thread's combined row is injected into, and their weights
+  const Inject& inj = p.inject;
+  const bool take_inject = combine && inj.out != nullptr && tid < RB && row0 + tid < H;
+  uint32_t r_hid[kMaxStreams], r_iw[kMaxStreams];
+#pragma unroll
+  for (int j = 0; j < static_cast<int>(kMaxStreams); ++j) {
+    const bool live = take_inject && static_cast<uint32_t>(j) < inj.hc;
+    r_hid[j] = live ? A::load_bits(inj.hidden, (static_cast<size_t>(t) * inj.hc + j) * H + row0 + tid) : 0u;
+    r_iw[j] = live ? A::load_bits(inj.weights, static_cast<size_t>(t) * inj.hc + j) : 0u;
+  }
 
   // 2. lane k < K resolves slot k; the waves take their slots' pointers with
   //    readlane and issue their weight loads
@@ -942,6 +952,14 @@ __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
         y = A::round(__fadd_rn(y, A::round(__fmul_rn(s_shared[r], s_sig))));
       }
       A::store(p.out, static_cast<size_t>(t) * H + row0 + r, y);
+      if (take_inject) {
+#pragma unroll
+        for (int j = 0; j < static_cast<int>(kMaxStreams); ++j) {
+          if (static_cast<uint32_t>(j) >= inj.hc) break;
+          const float v = A::round(__fadd_rn(A::from_bits(r_hid[j]), A::round(__fmul_rn(y, A::from_bits(r_iw[j])))));
+          A::store(inj.out, (static_cast<size_t>(t) * inj.hc + j) * H + row0 + r, v);
+        }
+      }
     }
   } else {
     for (uint32_t idx = tid; idx < K * RB; idx += kDownBlock) {

@@ -811,6 +811,30 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
   }
   *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + static_cast<size_t>(t) * p.hidden + h0) =
       make_uint4(out[0], out[1], out[2], out[3]);
+  // the hyper-connection injection of the 8 combined values into every stream
+  const Inject& inj = p.inject;
+  if (inj.out == nullptr) return;
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = bf16_to_f32(e & 1 ? out[e / 2] >> 16 : out[e / 2] & 0xffffu);
+  for (uint32_t j = 0; j < inj.hc; ++j) {
+    const size_t o = (static_cast<size_t>(t) * inj.hc + j) * p.hidden + h0;
+    const float w = ActBF16::load(inj.weights, static_cast<size_t>(t) * inj.hc + j);
+    const uint4 hv = ldg16(static_cast<const uint16_t*>(inj.hidden) + o);
+    const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
+    uint32_t res[4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      float v[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const float h = bf16_to_f32(k ? hw[e / 2] >> 16 : hw[e / 2] & 0xffffu);
+        v[k] = round_bf16(__fadd_rn(h, round_bf16(__fmul_rn(y[e + k], w))));
+      }
+      res[e / 2] = f32_to_bf16(v[0]) | (f32_to_bf16(v[1]) << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(inj.out) + o) = make_uint4(res[0], res[1], res[2], res[3]);
+  }
 }
 
 // ----------------------------------------------------------- shared gate ---

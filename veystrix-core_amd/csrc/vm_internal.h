@@ -60,6 +60,17 @@ struct GateUpLaunch {
   float blend;
 };
 
+// The hyper-connection injection of a branch output y [T, H] into hc residual
+// streams (compile_glue.py:32-35): out[t, j*H + h] = round(hidden[t, j*H + h]
+// + round(y[t, h] * weights[t, j])), activation dtype.  out == nullptr: off.
+constexpr uint32_t kMaxStreams = 8;
+struct Inject {
+  const void* hidden;          // [T, hc * H]
+  const void* weights;         // [T, hc]
+  void* out;                   // [T, hc * H], may be `hidden`
+  uint32_t hc;
+};
+
 struct DownLaunch {
   const void* act;             // [T, S, I]
   const uint32_t* routes;      // [T, K]
@@ -75,6 +86,7 @@ struct DownLaunch {
   const void* shared;          // [T, H]
   const void* shared_gate;     // [T]
   void* out;
+  Inject inject;               // optional injection of the combined rows into residual streams
   uint32_t* status;
   uint64_t* trace;             // optional phase timestamps, 8 per block
   uint32_t tokens, slots, hidden, inter, experts, has_shared;
@@ -184,6 +196,7 @@ struct CombineLaunch {
   const void* shared_sig;      // [tokens] bf16
   const void* shared_y;        // or a finished shared term [tokens, hidden] bf16
   void* out;                   // [tokens, hidden] bf16
+  Inject inject;               // modes 0 and 1: optional injection into residual streams
   uint32_t tokens, slots, hidden;
   int mode;                    // 0 fused combine, 1 generic combine, 2 per-slot rows
 };
@@ -230,5 +243,25 @@ struct PhaseTrace {
     r[14] = r[15] = 0;
   }
 };
+
+// ---------------------------------------------------------- decoder glue --
+constexpr uint32_t kHcMaxRow = 16384;     // hc * hidden
+constexpr uint32_t kHcMaxLowrank = 256;
+
+// The hyper-connection before a branch (glue.hip).
+struct HcLaunch {
+  const void* hidden;          // [T, n] the residual streams, n = hc * hidden
+  const void* norm_weight;     // [n] hc_norm gain
+  ProjPtrs down, up, inj;      // [lowrank, n/8], [n, lowrank/8], [hc, n/8] Q4/G32
+  void* normed;                // [T, n]
+  void* d;                     // [T, lowrank]
+  void* mixed;                 // [T, hidden]
+  void* weights;               // [T, hc]
+  float eps;
+  uint32_t tokens, width, hc, n, lowrank, norm_group, one_centered;  // width = hidden size
+  int act_dtype;
+};
+
+hipError_t launch_hyper_mix(const HcLaunch& p, hipStream_t stream);
 
 }  // namespace vm

@@ -106,11 +106,34 @@ class VmLayerArgs(ctypes.Structure):
         ("act_dtype", _c_u32),
         ("renorm_blend", ctypes.c_float),
         ("phases", _c_u32),
+        ("inject_hidden", _vp),
+        ("inject_weights", _vp),
+        ("inject_out", _vp),
+        ("hc_count", _c_u32),
+        ("reserved", _c_u32),
     ]
 
 
 VM_PHASE_ROUTER = 1
 VM_PHASE_EXPERTS = 2
+VM_MAX_STREAMS = 8
+
+
+class VmHyperArgs(ctypes.Structure):
+    _fields_ = [
+        ("hidden", _vp),
+        ("norm_weight", _vp),
+        ("mix_down", VmQ4Proj), ("mix_up", VmQ4Proj), ("inject", VmQ4Proj),
+        ("mixed", _vp),
+        ("weights", _vp),
+        ("normed", _vp),
+        ("workspace", _vp),
+        ("workspace_bytes", _c_u64),
+        ("tokens", _c_u32), ("hidden_size", _c_u32), ("hc_count", _c_u32), ("lowrank", _c_u32),
+        ("norm_group", _c_u32), ("one_centered", _c_u32),
+        ("act_dtype", _c_u32),
+        ("eps", ctypes.c_float),
+    ]
 
 
 class VmDeviceLru(ctypes.Structure):
@@ -161,6 +184,8 @@ SIGNATURES = {
     "vm_moe_layer_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_layer": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), _vp]),
     "vm_moe_layer_lru": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), ctypes.POINTER(VmDeviceLru), _vp]),
+    "vm_hyper_mix_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
+    "vm_hyper_mix": (ctypes.c_int, [ctypes.POINTER(VmHyperArgs), _vp]),
     "vm_moe_grouped_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_grouped": (ctypes.c_int, [ctypes.POINTER(VmGroupedArgs), _vp]),
     "vm_weighted_combine": (ctypes.c_int, [_vp, _vp, _vp, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _vp]),

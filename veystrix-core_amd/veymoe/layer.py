@@ -245,10 +245,15 @@ class MoELayer:
         a.renorm_blend = self.renorm_blend
         return a
 
-    def forward(self, flat: torch.Tensor) -> torch.Tensor:
+    def forward(self, flat: torch.Tensor, inject=None) -> torch.Tensor:
         """The layer on [rows, hidden]: rows <= 8 run the fused decode kernels,
         more rows the grouped path (router GEMM, device token-by-expert sort,
-        MFMA grouped experts, generic combine); both inside vm_moe_layer."""
+        MFMA grouped experts, generic combine); both inside vm_moe_layer.
+
+        ``inject = (streams [rows, hc*hidden], weights [rows, hc], out)``: the
+        experts' final epilogue also writes the hyper-connection injection of
+        the layer output into the residual streams (compile_glue.py:32-35)
+        into ``out`` (which may be ``streams``)."""
         require_device("x", flat, (torch.bfloat16, torch.float32))
         tokens = flat.shape[0]
         out = torch.empty_like(flat)
@@ -265,6 +270,7 @@ class MoELayer:
         args.x = ptr(flat)
         args.output = ptr(out)
         args.phases = 0
+        self._set_inject(args, flat, inject)
         lib = _lib.lib()
         sw = self.switch_mlp
         lru = sw.pool.device_lru if sw.pool is not None else None
@@ -274,7 +280,7 @@ class MoELayer:
                 # LRU state back for this call
                 sw.pool.detach_device_lru()
                 try:
-                    return self.forward(flat)
+                    return self.forward(flat, inject)
                 finally:
                     sw.pool.attach_device_lru(lru.store)
             if tokens * self.top_k > lru.usable_slots:
@@ -302,6 +308,27 @@ class MoELayer:
         _lib.check(lib.vm_moe_layer(args, stream_handle()))
         self.last_inds, self.last_scores = inds, scores
         return out
+
+    @staticmethod
+    def _set_inject(args, flat: torch.Tensor, inject) -> None:
+        if inject is None:
+            args.inject_hidden = args.inject_weights = args.inject_out = None
+            args.hc_count = 0
+            return
+        streams, weights, target = inject
+        rows = flat.shape[0]
+        for name, t in (("streams", streams), ("weights", weights), ("out", target)):
+            require_device(name, t, (flat.dtype,))
+            if not t.is_contiguous():
+                raise ValueError(f"{name} must be contiguous")
+        hc = weights.shape[-1]
+        if weights.numel() != rows * hc or streams.numel() != rows * hc * flat.shape[1] or \
+                target.numel() != streams.numel():
+            raise ValueError("injection shapes must be streams [rows, hc*hidden], weights [rows, hc]")
+        args.inject_hidden = ptr(streams)
+        args.inject_weights = ptr(weights)
+        args.inject_out = ptr(target)
+        args.hc_count = hc
 
     def _routes_to_host(self, inds: torch.Tensor) -> list:
         """The routed expert ids on the host: one D2H copy into a pinned
