@@ -345,6 +345,109 @@ def run_stack(seed, tokens=12, warm_tokens=12, store_records=2048, pool_bytes=6_
     return result
 
 
+def run_branch(stack, spec, steps, warmup, seed, moe_ms_per_step, hc=4, lowrank=32):
+    """The decoder layer's MLP branch around every layer of `stack` (batch 1):
+    the hyper-connection of the `hc` residual streams (vm_hyper_mix: RMSNorm,
+    low-rank Q4 mix, injection weights; qwen4_verifier.py:20-33), the MoE
+    layer, and the injection of its output into the streams written by the
+    experts' last epilogue (compile_glue.py:32-35).  One HIP graph per pass
+    over the layers, like the decode value; reports the time per layer and
+    what the glue adds to the MoE layer alone."""
+    import torch
+
+    from veymoe import _lib
+    from veymoe.device import q4proj, stream_handle
+
+    device = torch.device("cuda:0")
+    layers, H = len(stack), spec.hidden
+    n = hc * H
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed + 17)
+
+    def q4(out_w, in_w):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (out_w, in_w // 8), dtype=torch.int32, device=device, generator=gen)
+        sc = torch.empty((out_w, in_w // 32), device=device).uniform_(0.005, 0.02, generator=gen)
+        bi = torch.empty((out_w, in_w // 32), device=device).uniform_(-0.1, 0.1, generator=gen)
+        return w, sc.to(torch.bfloat16), bi.to(torch.bfloat16)
+
+    lib = _lib.lib()
+    streams = torch.randn((layers, 1, n), device=device, generator=gen).to(torch.bfloat16)
+    target = torch.empty_like(streams)
+    mixed = torch.empty((layers, 1, H), dtype=torch.bfloat16, device=device)
+    weights = torch.empty((layers, 1, hc), dtype=torch.bfloat16, device=device)
+    y = torch.empty_like(mixed)
+    inds = torch.empty((layers, 1, spec.top_k), dtype=torch.int32, device=device)
+    scores = torch.empty((layers, 1, spec.top_k), dtype=torch.bfloat16, device=device)
+    ws_bytes = int(lib.vm_hyper_mix_workspace(1, hc, H, lowrank, 0))
+    keep, calls = [], []
+    for i in range(layers):
+        gain = (1.0 + 0.2 * torch.randn(n, device=device, generator=gen)).to(torch.bfloat16)
+        down, up, inj = q4(lowrank, n), q4(n, lowrank), q4(hc, n)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        h = _lib.VmHyperArgs()
+        h.hidden, h.norm_weight = streams[i].data_ptr(), gain.data_ptr()
+        h.mix_down, h.mix_up, h.inject = q4proj(*down), q4proj(*up), q4proj(*inj)
+        h.mixed, h.weights = mixed[i].data_ptr(), weights[i].data_ptr()
+        h.workspace, h.workspace_bytes = ws.data_ptr(), ws_bytes
+        h.tokens, h.hidden_size, h.hc_count, h.lowrank, h.norm_group, h.one_centered = 1, H, hc, lowrank, 0, 1
+        h.eps = 1e-6
+        a = stack[i].layer_args(mixed[i], y[i], inds[i], scores[i])
+        a.inject_hidden, a.inject_weights, a.inject_out, a.hc_count = (
+            streams[i].data_ptr(), weights[i].data_ptr(), target[i].data_ptr(), hc)
+        keep += [gain, down, up, inj, ws, h, a]
+        calls.append((ctypes.byref(h), ctypes.byref(a)))
+    stream = torch.cuda.Stream(device=device)
+
+    def one_pass(handle):
+        for href, aref in calls:
+            _lib.check(lib.vm_hyper_mix(href, handle))
+            _lib.check(lib.vm_moe_layer(aref, handle))
+
+    with torch.cuda.stream(stream):
+        handle = stream_handle(stream)
+        for _ in range(max(1, warmup // layers)):
+            one_pass(handle)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            one_pass(stream_handle(torch.cuda.current_stream()))
+        for _ in range(4):
+            graph.replay()
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        for _ in range(steps // layers):
+            graph.replay()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - start
+    us = elapsed * 1e6 / steps
+    # the two hyper-connection kernels by their own dispatch events
+    lib.vm_timing_reset()
+    lib.vm_timing_enable(1)
+    with torch.cuda.stream(stream):
+        for _ in range(max(1, (steps // layers) // 4)):
+            one_pass(stream_handle(stream))
+    torch.cuda.synchronize()
+    lib.vm_timing_enable(0)
+    kernels = {}
+    for name in ("hc_front", "hc_up"):
+        total, launches = ctypes.c_double(), ctypes.c_uint64()
+        _lib.check(lib.vm_timing_read(name.encode(), ctypes.byref(total), ctypes.byref(launches)))
+        kernels[name] = round(total.value * 1e3 / max(1, launches.value), 3)
+    # streams and gain read, the Q4/G32 mix and injection rows (0.625 B per
+    # weight), normed written and read back, the streams read and written again
+    # by the injection
+    glue_bytes = 2 * n * 2 + ((lowrank + hc) * n + n * lowrank) * 5 // 8 + 2 * n * 2 + 2 * n * 2
+    result = {"hc_count": hc, "lowrank": lowrank, "us_per_layer": round(us, 2),
+              "moe_us_per_layer": round(moe_ms_per_step * 1e3, 2),
+              "glue_us_per_layer": round(us - moe_ms_per_step * 1e3, 2),
+              "glue_bytes_per_layer": glue_bytes, "kernels_us": kernels, "launch": "hipgraph",
+              "launches_per_layer": 5,
+              "note": "hyper-connection (2 launches) + MoE layer (3) with the stream injection in its last "
+                      "epilogue; the MoE figure is the decode value's step"}
+    del graph, keep, calls
+    return result
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     parser.add_argument("--gpus", type=int, default=1)
@@ -467,6 +570,8 @@ def main():
         "kernels": kernels,
         "roofline": roofline,
     }
+    log("decoder MLP branch: hyper-connection + MoE layer + stream injection")
+    result["decoder_branch"] = run_branch(stack, spec, steps, warmup, args.seed, ms_per_step)
     del graph, stack, pool, call_args, refs
     torch.cuda.empty_cache()
     if not args.no_grouped:

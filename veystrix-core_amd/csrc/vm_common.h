@@ -119,6 +119,13 @@ __device__ __forceinline__ float swiglu_act(float g, float u) {
   return A::round(s * u);
 }
 
+// Block barrier that orders LDS only: global stores stay in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // ---------------------------------------------------------- reductions ---
 // DPP controls (GFX9): quad_perm, row_half_mirror, row_mirror, row_bcast.
 constexpr int kDppQuadXor1 = 0xB1;     // quad_perm [1,0,3,2]
