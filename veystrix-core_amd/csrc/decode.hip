@@ -424,14 +424,14 @@ __global__ __launch_bounds__(64) void k_select_f32(SelectLaunch p) { select_body
 // order (vm_lru.h).
 static_assert(64 * kMaxExpertsPerLane <= kLruMaxExperts, "routed ids must fit the LRU's LDS map");
 
-template <class A>
+template <class A, int P>
 __global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruLaunch l) {
   __shared__ typename Cand<A>::T s_cands[kLruWaves][kMaxCand];
   __shared__ int32_t s_routed[kLruMaxRouted];
   __shared__ LruShared sh;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
-  LruRegs r;
+  LruRegs<P> r;
   lru_begin(l, sh, r);  // independent of the routing: in flight during the selection
   if (wave < p.tokens) {
     const uint32_t t = wave;
@@ -799,7 +799,9 @@ constexpr int kDownQuads = VM_DOWN_QUADS;                 // row groups of 64/LP
 
 // LPR = I/32 lanes per row (one group each); a block covers RB rows of all
 // slots of one token.
-template <class A, int LPR>
+// INJ: the combined rows are also injected into residual streams (p.inject);
+// a separate instance, so the plain kernel carries none of its loads.
+template <class A, int LPR, bool INJ>
 __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
   constexpr int RPI = 64 / LPR;
   constexpr int RB = RPI * kDownQuads;
@@ -861,13 +863,16 @@ __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
   if (take_sig) r_sig = A::load_bits(sig_src, t);
   // the streams this thread's combined row is injected into, and their weights
   const Inject& inj = p.inject;
-  const bool take_inject = combine && inj.out != nullptr && tid < RB && row0 + tid < H;
-  uint32_t r_hid[kMaxStreams], r_iw[kMaxStreams];
+  const bool take_inject = INJ && combine && tid < RB && row0 + tid < H;
+  constexpr int kStreams = INJ ? static_cast<int>(kMaxStreams) : 1;
+  uint32_t r_hid[kStreams], r_iw[kStreams];
+  if constexpr (INJ) {
 #pragma unroll
-  for (int j = 0; j < static_cast<int>(kMaxStreams); ++j) {
-    const bool live = take_inject && static_cast<uint32_t>(j) < inj.hc;
-    r_hid[j] = live ? A::load_bits(inj.hidden, (static_cast<size_t>(t) * inj.hc + j) * H + row0 + tid) : 0u;
-    r_iw[j] = live ? A::load_bits(inj.weights, static_cast<size_t>(t) * inj.hc + j) : 0u;
+    for (int j = 0; j < kStreams; ++j) {
+      const bool live = take_inject && static_cast<uint32_t>(j) < inj.hc;
+      r_hid[j] = live ? A::load_bits(inj.hidden, (static_cast<size_t>(t) * inj.hc + j) * H + row0 + tid) : 0u;
+      r_iw[j] = live ? A::load_bits(inj.weights, static_cast<size_t>(t) * inj.hc + j) : 0u;
+    }
   }
 
   // 2. lane k < K resolves slot k; the waves take their slots' pointers with
@@ -952,9 +957,9 @@ __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
         y = A::round(__fadd_rn(y, A::round(__fmul_rn(s_shared[r], s_sig))));
       }
       A::store(p.out, static_cast<size_t>(t) * H + row0 + r, y);
-      if (take_inject) {
+      if (INJ && take_inject) {
 #pragma unroll
-        for (int j = 0; j < static_cast<int>(kMaxStreams); ++j) {
+        for (int j = 0; j < kStreams; ++j) {
           if (static_cast<uint32_t>(j) >= inj.hc) break;
           const float v = A::round(__fadd_rn(A::from_bits(r_hid[j]), A::round(__fmul_rn(y, A::from_bits(r_iw[j])))));
           A::store(inj.out, (static_cast<size_t>(t) * inj.hc + j) * H + row0 + r, v);
@@ -1046,7 +1051,8 @@ hipError_t down_go(const DownLaunch& p, hipStream_t stream) {
   dim3 grid((p.hidden + RB - 1) / RB, p.tokens);
   DownLaunch q = p;
   q.trace = trace_reserve(grid.x * grid.y);
-  return launch("down", k_down<A, LPR>, grid, dim3(kDownBlock), stream, q);
+  if (p.inject.out != nullptr) return launch("down", k_down<A, LPR, true>, grid, dim3(kDownBlock), stream, q);
+  return launch("down", k_down<A, LPR, false>, grid, dim3(kDownBlock), stream, q);
 }
 
 template <class A>
@@ -1093,10 +1099,24 @@ hipError_t launch_front(const FrontLaunch& p, hipStream_t stream) {
   return p.act_dtype == 0 ? front_go<ActBF16>(p, stream) : front_go<ActF32>(p, stream);
 }
 
-hipError_t launch_select_lru(const SelectLaunch& p, const LruLaunch& l, hipStream_t stream) {
+template <int P>
+hipError_t select_lru_go(const SelectLaunch& p, const LruLaunch& l, hipStream_t stream) {
   const dim3 grid(1), block(kLruThreads);
-  return p.act_dtype == 0 ? launch("lru", k_select_lru<ActBF16>, grid, block, stream, p, l)
-                          : launch("lru", k_select_lru<ActF32>, grid, block, stream, p, l);
+  return p.act_dtype == 0 ? launch("lru", k_select_lru<ActBF16, P>, grid, block, stream, p, l)
+                          : launch("lru", k_select_lru<ActF32, P>, grid, block, stream, p, l);
+}
+
+hipError_t launch_select_lru(const SelectLaunch& p, const LruLaunch& l, hipStream_t stream) {
+  // queue entries per thread, rounded up to the instantiated powers of two
+  const uint32_t per = (l.order_len + kLruThreads - 1) / kLruThreads;
+  static_assert(kLruSlotsPerThread == 32, "instances below cover 1..32 entries per thread");
+  if (per <= 1) return select_lru_go<1>(p, l, stream);
+  if (per <= 2) return select_lru_go<2>(p, l, stream);
+  if (per <= 4) return select_lru_go<4>(p, l, stream);
+  if (per <= 8) return select_lru_go<8>(p, l, stream);
+  if (per <= 16) return select_lru_go<16>(p, l, stream);
+  if (per <= 32) return select_lru_go<32>(p, l, stream);
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_select(const SelectLaunch& p, hipStream_t stream) {

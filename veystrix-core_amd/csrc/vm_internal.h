@@ -86,11 +86,13 @@ struct DownLaunch {
   const void* shared;          // [T, H]
   const void* shared_gate;     // [T]
   void* out;
-  Inject inject;               // optional injection of the combined rows into residual streams
   uint32_t* status;
   uint64_t* trace;             // optional phase timestamps, 8 per block
   uint32_t tokens, slots, hidden, inter, experts, has_shared;
   int act_dtype;
+  // Last, so that the fields above keep the kernel-argument offsets the
+  // kernel's scalar loads are scheduled around.
+  Inject inject;               // optional injection of the combined rows into residual streams
 };
 
 // ------------------------------------------------------ device-side LRU --
@@ -196,9 +198,9 @@ struct CombineLaunch {
   const void* shared_sig;      // [tokens] bf16
   const void* shared_y;        // or a finished shared term [tokens, hidden] bf16
   void* out;                   // [tokens, hidden] bf16
-  Inject inject;               // modes 0 and 1: optional injection into residual streams
   uint32_t tokens, slots, hidden;
   int mode;                    // 0 fused combine, 1 generic combine, 2 per-slot rows
+  Inject inject;               // modes 0 and 1: optional injection into residual streams
 };
 
 // Upper bound of the tiles of `tile_rows` rows over `groups` groups holding `rows` rows.

@@ -45,10 +45,15 @@ struct LruShared {
   uint32_t hits, misses, valid;
 };
 
-// Per-thread state loaded before the routed ids are known.
+// Per-thread state loaded before the routed ids are known.  P bounds the
+// queue entries a thread holds (at least ceil(order_len / kLruThreads)): the
+// per-entry loops run P iterations, so the kernel is instantiated for the
+// powers of two up to kLruSlotsPerThread and launched with the smallest that
+// fits the queue.
+template <int P>
 struct LruRegs {
-  int32_t q[kLruSlotsPerThread];     // queue entries lo .. lo + n - 1
-  int32_t own[kLruSlotsPerThread];   // owners of those slots
+  int32_t q[P];                      // queue entries lo .. lo + n - 1
+  int32_t own[P];                    // owners of those slots
   uint32_t lo, n;
   uint64_t counter;                  // wave 0, lanes 0..7: counters[0..3], then the layer's four
 };
@@ -71,16 +76,17 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v, uint32_t lane
 // Every thread, before the selection: clear the LDS maps, load this thread's
 // run of the queue and (wave 0) the counters.  A block barrier must separate
 // it from lru_assign.
-__device__ __forceinline__ void lru_begin(const LruLaunch& p, LruShared& sh, LruRegs& r) {
+template <int P>
+__device__ __forceinline__ void lru_begin(const LruLaunch& p, LruShared& sh, LruRegs<P>& r) {
   const uint32_t tid = threadIdx.x;
   if (tid < kLruMaxExperts) sh.first[tid] = ~0u;
   sh.hit_bits[tid] = 0;
   const uint32_t U = p.order_len;
-  const uint32_t per = (U + kLruThreads - 1) / kLruThreads;  // <= kLruSlotsPerThread
+  const uint32_t per = (U + kLruThreads - 1) / kLruThreads;  // <= P
   r.lo = tid * per;
   r.n = r.lo < U ? min(per, U - r.lo) : 0u;
 #pragma unroll
-  for (int i = 0; i < kLruSlotsPerThread; ++i)
+  for (int i = 0; i < P; ++i)
     r.q[i] = static_cast<uint32_t>(i) < r.n ? p.lru_order[r.lo + i] : -1;
   const uint32_t lane = tid & 63u;
   r.counter = 0;
@@ -90,9 +96,10 @@ __device__ __forceinline__ void lru_begin(const LruLaunch& p, LruShared& sh, Lru
 // Every thread, after the selection (its registers are free by then): the
 // owners of this thread's queue entries, in flight while wave 0 looks up the
 // routed ids.
-__device__ __forceinline__ void lru_owners(const LruLaunch& p, LruRegs& r) {
+template <int P>
+__device__ __forceinline__ void lru_owners(const LruLaunch& p, LruRegs<P>& r) {
 #pragma unroll
-  for (int i = 0; i < kLruSlotsPerThread; ++i) {
+  for (int i = 0; i < P; ++i) {
     const int32_t s = r.q[i];
     r.own[i] = static_cast<uint32_t>(i) < r.n && s >= 0 && static_cast<uint32_t>(s) < p.slots ? p.slot_owner[s] : -1;
   }
@@ -100,7 +107,8 @@ __device__ __forceinline__ void lru_owners(const LruLaunch& p, LruRegs& r) {
 
 // assign() of the routed ids in `routed` (LDS, -1 = skipped) for one call.
 // Every thread of the block must call it (it holds block barriers).
-__device__ void lru_assign(const LruLaunch& p, const int32_t* routed, LruShared& sh, LruRegs& r) {
+template <int P>
+__device__ void lru_assign(const LruLaunch& p, const int32_t* routed, LruShared& sh, LruRegs<P>& r) {
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
@@ -169,7 +177,7 @@ __device__ void lru_assign(const LruLaunch& p, const int32_t* routed, LruShared&
   //    the kept entries within the wave, wave totals to LDS
   uint32_t keep_mask = 0, keep = 0, hitq = 0, bad = 0;
 #pragma unroll
-  for (int i = 0; i < kLruSlotsPerThread; ++i) {
+  for (int i = 0; i < P; ++i) {
     if (static_cast<uint32_t>(i) < r.n) {
       const int32_t s = r.q[i];
       if (s < 0 || static_cast<uint32_t>(s) >= S) {
@@ -211,7 +219,7 @@ __device__ void lru_assign(const LruLaunch& p, const int32_t* routed, LruShared&
   const uint32_t kept = NH - found;
   uint32_t rank = (before + incl - packed) & 0xffffu;
 #pragma unroll
-  for (int i = 0; i < kLruSlotsPerThread; ++i) {
+  for (int i = 0; i < P; ++i) {
     if ((keep_mask >> i) & 1u) {
       if (rank < found) {
         sh.victim[rank] = r.q[i];
