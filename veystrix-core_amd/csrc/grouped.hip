@@ -17,7 +17,8 @@
 //            buffered): the A rows (32 lanes per 512-byte row segment,
 //            pair-permuted to match the dequantised weights), the Q4 weight
 //            row chunks (8 lanes per 128-byte line) and the scale and bias
-//            vectors.  Each lane dequantises its 16-byte Q4 groups into bf16
+//            vectors; the 16-byte units of A rows and weight lines are
+//            XOR-swizzled so the MFMA lanes' LDS reads are conflict-free.  Each lane dequantises its 16-byte Q4 groups into bf16
 //            (f16 magic number + v_fma_mix + v_cvt_pk_bf16_f32) and feeds
 //            v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The MFMA loop
 //            is specialised on the number of 16-row blocks in use, so it has
@@ -52,7 +53,29 @@ constexpr int kCG = VM_GCG;              // 32-input groups per K chunk (8: a 12
 static_assert(kCG == 8, "the scale and bias staging covers exactly eight groups per chunk");
 constexpr int kHalves = kCG / 4;         // groups per lane and chunk
 constexpr int kSteps = 4 * kHalves;      // MFMA k steps per chunk
-constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 against bank conflicts)
+
+// LDS layouts of the staged A rows and weight lines.  A wave64 ds_read_b128
+// serves 16 lanes per cycle from 64 four-byte banks, and the lanes it serves
+// together are not 16 consecutive ones: a row padding of 16 bytes (the usual
+// remedy) left both the MFMA A reads (lane = row am, k block akb) and the
+// weight-line reads (lane = column bn, group bkb) two-way conflicted, 8.2
+// cycles per wave read instead of 4.5 in a timing of each read pattern.
+// XORing the 16-byte unit index with bits of the row (column) makes every
+// read step of both loops conflict-free in the same timing and needs no
+// padding.  A row r stores its logical unit u at unit u ^ a_swz(r); the
+// swizzle depends on r mod 16 only, the row within an MFMA block.  The XOR
+// reaches the step bits of the unit, so each read step needs an address of
+// its own: in the down GEMM the extra registers cost its second block per CU
+// (40 % slower), so its rows keep the padded layout, whose step offsets are
+// immediates.
+template <int EPI>
+constexpr bool swz_rows() { return EPI != kEpiRows; }
+// LDS bytes per staged A row
+template <int EPI>
+constexpr int row_bytes() { return swz_rows<EPI>() ? kCG * 64 : kCG * 64 + 16; }
+__device__ __forceinline__ constexpr uint32_t a_swz(uint32_t r) { return (r & 3u) | ((r & 12u) << 1); }
+// A weight line of column c stores its group g at unit g ^ w_swz(c).
+__device__ __forceinline__ constexpr uint32_t w_swz(uint32_t c) { return c & 7u; }
 
 // Bytes of one LDS stage of a grouped GEMM instance: the A rows, then for Q4
 // weights without a tail chunk the chunk's scale and bias vectors of every
@@ -65,7 +88,7 @@ constexpr int kRowBytes = kCG * 64 + 16; // LDS bytes per staged row (+16 agains
 #ifndef VM_LDS_B_DN
 #define VM_LDS_B_DN 0
 #endif
-constexpr int kWColBytes = kCG * 16 + 16;  // LDS bytes per staged weight row chunk (+16 against bank conflicts)
+constexpr int kWColBytes = kCG * 16;  // LDS bytes per staged weight row chunk (unpadded: the groups are swizzled)
 
 // Q4 weights staged through LDS (coalesced 128-byte row loads by the whole
 // block) rather than loaded by the MFMA lanes themselves.
@@ -82,7 +105,7 @@ constexpr int tile_rows() {
 
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 constexpr int stage_bytes() {
-  return tile_rows<EPI>() * kRowBytes + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
+  return tile_rows<EPI>() * row_bytes<EPI>() + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
          (lds_weights<EPI, TAIL>() ? PROJ * WAVES * NBW * 16 * kWColBytes : 0);
 }
 
@@ -246,6 +269,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr int kItems = (kItemsAll + kThreads - 1) / kThreads;  // per thread
   constexpr bool kAllItems = kItemsAll % kThreads == 0;
 
+  constexpr bool kSwz = swz_rows<EPI>();
+  constexpr int kRowB = row_bytes<EPI>();
   const uint32_t tid = threadIdx.x;
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
@@ -267,7 +292,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     const uint32_t arow = p.row_token != nullptr ? p.row_token[row0 + rr] : row0 + rr;
     a_src[j] = p.a + static_cast<size_t>(arow) * p.a_stride + u * 8;
     a_u[j] = u;
-    a_off[j] = r * kRowBytes + u * 16;
+    a_off[j] = r * kRowB + (u ^ (kSwz ? a_swz(r) : 0u)) * 16;
   }
   // scale staging (Q4, full chunks): vector v = tid + j * threads -> (proj,
   // scales or biases, column of the block); 16 bytes = the chunk's 8 groups
@@ -276,7 +301,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr int kSVecs = kLdsScales ? PROJ * 2 * kCols : 0;
   constexpr int kSItems = (kSVecs + kThreads - 1) / kThreads;
   constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
-  constexpr int kStageBytes = tile_rows<EPI>() * kRowBytes;  // the A rows of a stage
+  constexpr int kStageBytes = tile_rows<EPI>() * kRowB;  // the A rows of a stage
   const uint16_t* sv_src[kSItems > 0 ? kSItems : 1];
 #pragma unroll
   for (int j = 0; j < kSItems; ++j) {
@@ -312,7 +337,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     const uint32_t ci = (it % kPerProj) / kCG, g = it % kCG;
     const uint32_t col = min(slice * kCols + ci, N - 1);
     w_src[j] = reinterpret_cast<const uint8_t*>(w[pj].w) + static_cast<size_t>(col) * (K / 2) + g * 16u;
-    w_off[j] = kWArea + (pj * kCols + ci) * kWColBytes + g * 16u;
+    w_off[j] = kWArea + (pj * kCols + ci) * kWColBytes + (g ^ w_swz(ci)) * 16u;
   }
   uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1], wr[kWItems > 0 ? kWItems : 1];
   auto a_load = [&](uint32_t g0, bool tail) {
@@ -381,9 +406,12 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   const uint32_t chunks = (G + kCG - 1) / kCG;
   const uint32_t magic = Q4 ? f16_magic() : 0u;
   const uint32_t am = lane & 15u, akb = lane >> 4;
-  const uint32_t a_lane = am * kRowBytes + akb * 64;
+  // the lane's unit of step st is (16 (st / 4) + 4 akb + st % 4) ^ a_swz(am);
+  // the three terms occupy disjoint bits, so the step's part is XORed on last
+  const uint32_t a_lane = am * kRowB + ((akb * 4) ^ (kSwz ? a_swz(am) : 0u)) * 16;
+  const uint32_t w_lane = (bkb ^ w_swz(bn)) * 16;  // the group part of the weight-line reads
   auto compute = [&](int buf, const BChunk<Q4, TAIL> (&bc)[PROJ][NBW]) {
-    const uint8_t* s_a = s_a0 + buf * kStage + a_lane;
+    const uint8_t* s_a = s_a0 + buf * kStage;
     BChunk<Q4, TAIL> bl[PROJ][NBW];
     uint32_t s2[PROJ][NBW], b2[PROJ][NBW];
 #pragma unroll
@@ -400,11 +428,12 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       }
 #pragma unroll
     for (int st = 0; st < kSteps; ++st) {
+      const uint32_t a_step = (st >> 2) * 256u + (st & 3) * 16u;
       bf16x8_t aop[MBU];
 #pragma unroll
       for (int mb = 0; mb < MBU; ++mb)
         aop[mb] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(
-                                                   s_a + mb * 16 * kRowBytes + (st >> 2) * 256 + (st & 3) * 16));
+                                                   s_a + mb * 16 * kRowB + (kSwz ? a_lane ^ a_step : a_lane + a_step)));
       if constexpr (kLdsB) {
         if ((st & 3) == 0) {  // the lane's group 4 h + kb of each of its rows, from LDS
 #pragma unroll
@@ -413,7 +442,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
             for (int nb = 0; nb < NBW; ++nb) {
               const uint32_t col = wave * NBW * 16 + nb * 16 + bn;
               bl[pj][nb].w[st >> 2] = *reinterpret_cast<const uint4*>(
-                  s_a0 + buf * kStage + kWArea + (pj * kCols + col) * kWColBytes + ((st >> 2) * 4 + bkb) * 16);
+                  s_a0 + buf * kStage + kWArea + (pj * kCols + col) * kWColBytes + (w_lane ^ ((st >> 2) * 64u)));
             }
         }
       }
@@ -492,6 +521,9 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #ifndef VM_G_WAVES_PER_EU
 #define VM_G_WAVES_PER_EU 1
 #endif
+// The down GEMM runs two 8-wave blocks per CU (its LDS allows two): four waves
+// per SIMD, so its VGPRs must stay at or below 128.  Above that only one block
+// fits and the kernel takes 40 % longer.
 #ifndef VM_DN_WAVES_PER_EU
 #define VM_DN_WAVES_PER_EU 2
 #endif
