@@ -467,8 +467,10 @@ def main():
                              "(out = in * 1): the reference reading for HBM byte counters")
     args = parser.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
-              "(the path is single-GPU; see the sharding notes in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the MoE layer "
+              "path runs on one GPU, and sharding it across GPUs (by requests or layers for "
+              "decode, by experts with an all-to-all of the routed rows for prefill) is not "
+              "built", file=sys.stderr)
         sys.exit(2)
 
     import torch
