@@ -6,27 +6,33 @@ Workload (the full-size decode layer): hidden 2048, expert intermediate 512,
 4-bit affine group-32 experts (uniform nibbles, bf16 scales U(0.005, 0.02),
 bf16 biases U(-0.1, 0.1)), bf16 router N(0, 0.02), bf16 activations N(0, 1);
 every expert resident in one HBM pool at a random slot behind an int32 slot
-table.  A step is one token through one MoE layer (router, slot lookup,
-shared expert, ten routed experts, combine).  Steps cycle through --layers
-distinct layers (48 by default, 48 GB of expert records) so the 256 MB
-Infinity Cache cannot serve repeated weights; inputs are resident in HBM.
+table.  A layer-token is one token through one MoE layer (router, slot
+lookup, shared expert, ten routed experts, combine).
 
-value = layer-tokens/s over the timed steps (graph replay of one pass over
-the layers per replay, unless --eager).  roofline: the gate/up kernel (the
-largest HBM consumer) timed with HIP start/stop events attached to its own
-dispatches (hipExtLaunchKernelGGL) in a second, eager pass over the same
-steps; bytes = algorithmic bytes of one launch.  cpu_baseline:
-the C restatement of the same layer (oracle/cmoe.c, OpenMP) on a bounded
-sample of tokens, on this host's cores.
+A step is one decode token through --layers distinct layers (48 by default,
+48 GB of expert records, so the 256 MB Infinity Cache cannot serve repeated
+weights): one HIP graph replay, unless --eager.  --warmup untimed steps, then
+exactly --steps timed steps between HIP events, synchronised on both sides.
+value = layer-tokens/s = steps * layers / time; ms_per_step is per replay.
+Inputs are resident in HBM.
 
-Extra fields (not `value`): "batched" (32 rows per call, Zipf(1.1) routing,
-8 pool-resident layers cycled) and "prefill" (2048 rows per call, 3 layers
-cycled) through the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA
-fraction (algorithmic FLOPs / time / 2.5 PFLOP/s); "prefill_window" (the
-layer-major order: four 2048-row chunks in one layer call, each expert read
-once per window); "stack48_lru" (48 layers at
-batch 1 with a 3,051-slot LRU pool, Zipf routing, misses staged from pinned
-host memory): tokens/s through the stack, hit rate, staged bytes.
+roofline: the gate/up kernel (the largest HBM consumer) timed with HIP
+start/stop events attached to its own dispatches (hipExtLaunchKernelGGL) in a
+second, eager pass over the same steps; bytes = algorithmic bytes of one
+launch.  cpu_baseline: the C restatement of the same layer (oracle/cmoe.c,
+OpenMP) on a bounded sample of tokens, on this host's cores.
+
+Extra fields (not `value`): "decode_small" (hidden 1024 / inter 256 / 64
+experts top-4 at batch 1 over 256 layers, with the NumPy oracle's time per
+token); "batched" (32 rows per call, Zipf(1.1) routing, 8 pool-resident
+layers cycled) and "prefill" (2048 rows per call, 3 layers cycled) through
+the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA fraction
+(algorithmic FLOPs / time / 2.5 PFLOP/s); "prefill_window" (the layer-major
+order: four 2048-row chunks in one layer call, each expert read once per
+window); "stack48_lru" (48 layers at batch 1 with a 3,051-slot LRU pool,
+Zipf routing, misses staged from pinned host memory): tokens/s through the
+stack, hit rate, staged bytes; "custom_executor" with --custom-executor
+module:attr (the reference harness's plug-in convention).
 """
 from __future__ import annotations
 
@@ -82,11 +88,14 @@ def build_stack(spec, layers, device, seed):
         router = (torch.randn((spec.experts, spec.hidden), device=device, generator=gen) * 0.02).to(torch.bfloat16)
         bias = synth.router_bias(spec, seed, layer)   # log Zipf(s) popularity when the spec asks for it
         bias = None if bias is None else torch.from_numpy(bias).to(device)
-        shared = QuantizedMLP(q4(1, spec.shared_inter, spec.hidden), q4(1, spec.shared_inter, spec.hidden),
-                              q4(1, spec.hidden, spec.shared_inter))
+        shared = gate = None
+        if spec.shared_inter:
+            shared = QuantizedMLP(q4(1, spec.shared_inter, spec.hidden), q4(1, spec.shared_inter, spec.hidden),
+                                  q4(1, spec.hidden, spec.shared_inter))
+            gate = q4(1, 1, spec.hidden)
         switch = HipSwitchGLU(spec.hidden, spec.inter, spec.experts, pool=pool, layer_id=layer)
         stack.append(MoELayer(RouterLinear(router, bias), switch, spec.top_k, shared_expert=shared,
-                              shared_expert_gate=q4(1, 1, spec.hidden)))
+                              shared_expert_gate=gate))
     return stack, pool
 
 
@@ -95,7 +104,7 @@ def algorithmic_bytes(spec):
     expert = spec.layout.record_bytes                       # 1.875 * I * H
     proj = expert // 3                                      # one projection
     shared = expert if spec.shared_inter else 0
-    seg = spec.hidden // 2 + 2 * (spec.hidden // 32) * 2    # H -> 1 Q4 gate
+    seg = spec.hidden // 2 + 2 * (spec.hidden // 32) * 2 if spec.shared_inter else 0   # H -> 1 Q4 gate
     router = spec.experts * spec.hidden * 2
     xy = 2 * spec.hidden * 2
     layer = spec.top_k * expert + shared + seg + router + xy + spec.top_k * 8
@@ -139,8 +148,20 @@ def cpu_baseline(spec, seed, seconds):
         if elapsed >= seconds:
             break
     return {"value": round(count / elapsed, 2), "unit": "tok/s", "cores": threads(), "kind": "port",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
             "sample": f"{count} decode tokens through one layer of the same shape ({elapsed:.1f} s), "
-                      f"C restatement oracle/cmoe.c with OpenMP"}
+                      f"C restatement oracle/cmoe.c with OpenMP on {threads()} threads"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 BF16_MFMA_PEAK_TFLOPS = 2500.0
@@ -405,26 +426,25 @@ def run_branch(stack, spec, steps, warmup, seed, moe_ms_per_step, hc=4, lowrank=
 
     with torch.cuda.stream(stream):
         handle = stream_handle(stream)
-        for _ in range(max(1, warmup // layers)):
-            one_pass(handle)
+        one_pass(handle)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=stream):
             one_pass(stream_handle(torch.cuda.current_stream()))
-        for _ in range(4):
+        for _ in range(max(1, warmup)):
             graph.replay()
         torch.cuda.synchronize()
         start = time.perf_counter()
-        for _ in range(steps // layers):
+        for _ in range(steps):
             graph.replay()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - start
-    us = elapsed * 1e6 / steps
+    us = elapsed * 1e6 / (steps * layers)
     # the two hyper-connection kernels by their own dispatch events
     lib.vm_timing_reset()
     lib.vm_timing_enable(1)
     with torch.cuda.stream(stream):
-        for _ in range(max(1, (steps // layers) // 4)):
+        for _ in range(max(1, steps // 4)):
             one_pass(stream_handle(stream))
     torch.cuda.synchronize()
     lib.vm_timing_enable(0)
@@ -448,44 +468,22 @@ def run_branch(stack, spec, steps, warmup, seed, moe_ms_per_step, hc=4, lowrank=
     return result
 
 
-def main():
-    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=24000)
-    parser.add_argument("--warmup", type=int, default=2400)
-    parser.add_argument("--layers", type=int, default=48)
-    parser.add_argument("--seed", type=int, default=2026)
-    parser.add_argument("--eager", action="store_true", help="launch layer by layer instead of graph replay")
-    parser.add_argument("--cpu-seconds", type=float, default=12.0)
-    parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-grouped", action="store_true",
-                        help="skip the batched (32 rows) and prefill (2048 rows) grouped workloads")
-    parser.add_argument("--no-stack", action="store_true",
-                        help="skip the 48-layer stack with the LRU pool and host-staged misses")
-    parser.add_argument("--copy-probe-mib", type=int, default=0,
-                        help="after the timed work, stream this many MiB through one elementwise bf16 kernel "
-                             "(out = in * 1): the reference reading for HBM byte counters")
-    args = parser.parse_args()
-    if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the MoE layer "
-              "path runs on one GPU, and sharding it across GPUs (by requests or layers for "
-              "decode, by experts with an all-to-all of the routed rows for prefill) is not "
-              "built", file=sys.stderr)
-        sys.exit(2)
-
+def run_decode(spec, layers, steps, warmup, seed, eager=False):
+    """Decode timing of ``spec`` at batch 1 over ``layers`` pool-resident
+    layers.  A step is one pass of one token through every layer (one graph
+    replay unless ``eager``); ``warmup`` untimed steps, then exactly ``steps``
+    timed steps between HIP events on the replay stream, with a
+    synchronisation on both sides.  A second, eager pass over the same steps
+    times each kernel family by HIP events attached to its own dispatches."""
     import torch
 
-    from veymoe import _lib, synth
+    from veymoe import _lib
     from veymoe.device import stream_handle
 
     device = torch.device("cuda:0")
-    spec = synth.CONFIGS["decode"]
-    layers = args.layers
-    steps = max(layers, (args.steps // layers) * layers)
-    warmup = max(layers, (args.warmup // layers) * layers)
-    log(f"building {layers} layers ({layers * spec.experts} expert records, "
+    log(f"building {layers} layers of {spec.name} ({layers * spec.experts} expert records, "
         f"{layers * spec.experts * spec.layout.record_stride / 1e9:.1f} GB)")
-    stack, pool = build_stack(spec, layers, device, args.seed)
+    stack, pool = build_stack(spec, layers, device, seed)
     lib = _lib.lib()
     x = torch.randn((layers, 1, spec.hidden), device=device).to(torch.bfloat16)
     out = torch.empty_like(x)
@@ -504,58 +502,202 @@ def main():
 
     with torch.cuda.stream(stream):
         handle = stream_handle(stream)
-        for _ in range(warmup // layers):
-            one_pass(handle)
+        one_pass(handle)                 # workspaces touched before capture
         torch.cuda.synchronize()
         graph = None
-        if not args.eager:
+        if not eager:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 one_pass(stream_handle(torch.cuda.current_stream()))
-            for _ in range(4):
-                graph.replay()
-            torch.cuda.synchronize()
-        log(f"timing {steps} steps ({'graph' if graph is not None else 'eager'})")
-        torch.cuda.synchronize()
-        start = time.perf_counter()
-        for _ in range(steps // layers):
+
+        def step():
             if graph is not None:
                 graph.replay()
             else:
                 one_pass(handle)
+
+        for _ in range(warmup):
+            step()
+        log(f"timing {steps} steps of {layers} layers ({'graph' if graph is not None else 'eager'})")
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        elapsed = time.perf_counter() - start
-        ms_per_step = elapsed * 1e3 / steps
+        wall0 = time.perf_counter()
+        begin.record(stream)
+        for _ in range(steps):
+            step()
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+        elapsed = begin.elapsed_time(end) / 1e3
 
         # roofline pass: same steps, eager, HIP events stamped by each kernel's own dispatch
         lib.vm_timing_reset()
         lib.vm_timing_enable(1)
-        for _ in range(steps // layers):
+        for _ in range(steps):
             one_pass(handle)
         torch.cuda.synchronize()
         lib.vm_timing_enable(0)
     kernels = {}
-    for name in ("router", "gateup", "down"):
+    for name in KERNEL_FAMILIES:
         total, launches = ctypes.c_double(), ctypes.c_uint64()
         _lib.check(lib.vm_timing_read(name.encode(), ctypes.byref(total), ctypes.byref(launches)))
-        kernels[name] = {"avg_us": round(total.value * 1e3 / max(1, launches.value), 3),
-                         "launches": int(launches.value)}
+        if launches.value:
+            kernels[name] = {"avg_us": round(total.value * 1e3 / launches.value, 3), "launches": int(launches.value)}
     nbytes = algorithmic_bytes(spec)
     for name in kernels:
-        kernels[name]["bytes"] = nbytes[name]
-        kernels[name]["gbps"] = round(nbytes[name] / (kernels[name]["avg_us"] * 1e3), 1)
-    gateup = kernels["gateup"]
-    roofline = {"bound": "hbm", "kernel": "gateup (routed + shared gate/up Q4 GEMV + SwiGLU)",
-                "achieved": gateup["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(gateup["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic()}
+        if name in nbytes:
+            kernels[name]["bytes"] = nbytes[name]
+            kernels[name]["gbps"] = round(nbytes[name] / (kernels[name]["avg_us"] * 1e3), 1)
+    layer_s = elapsed / (steps * layers)
+    timing = {"elapsed_s": elapsed, "wall_s": wall, "layer_s": layer_s, "launch": "hipgraph" if graph else "eager",
+              "pool_gb": round(pool.buffer.numel() / 1e9, 2), "kernels": kernels, "bytes": nbytes}
+    return timing, stack, pool, graph
+
+
+def run_custom_executor(target_spec, seed, calls=200):
+    """The reference harness's --custom-executor arm (bench_runtime_layer.py:
+    515-640) at the decode shape: the ten routed experts of one token as a
+    compact bank, this package's executor as the built-in arm, the custom
+    runner validated against it and both timed with HIP events."""
+    import numpy as np
+    import torch
+
+    from veymoe import plugin, synth
+    from veymoe.executor import HipMoEExecutor, Q4G32Projection
+
+    target, reason = plugin.load_custom_executor(target_spec)
+    result = {"target": target_spec}
+    if target is None:
+        result["skipped"] = reason
+        return result
+    device = torch.device("cuda:0")
+    spec = synth.CONFIGS["decode"]
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    k, H, I = spec.top_k, spec.hidden, spec.inter
+
+    def q4(out_w, in_w):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (k, out_w, in_w // 8), dtype=torch.int32, device=device,
+                          generator=gen)
+        sc = torch.empty((k, out_w, in_w // 32), device=device).uniform_(0.005, 0.02, generator=gen)
+        bi = torch.empty((k, out_w, in_w // 32), device=device).uniform_(-0.1, 0.1, generator=gen)
+        return Q4G32Projection(w, sc.to(torch.bfloat16), bi.to(torch.bfloat16))
+
+    packs = {"gate_proj": q4(I, H), "up_proj": q4(I, H), "down_proj": q4(H, I)}
+    x = torch.randn((1, 1, H), device=device, generator=gen).to(torch.bfloat16)
+    routes = torch.arange(k, dtype=torch.int32, device=device).reshape(1, 1, k)
+    raw = torch.rand((1, 1, k), device=device, generator=gen) + 0.1
+    scores = (raw / raw.sum(-1, keepdim=True)).to(torch.bfloat16)
+    ids = np.random.default_rng(seed).choice(spec.experts, k, replace=False)
+    context = plugin.make_context(x, packs, routes, ids, scores, hidden_size=H, top_k=k)
+    builtin = HipMoEExecutor(k, H, k)
+    want = plugin.run_custom(builtin, context)
+    runner = plugin.runner_from_target(target, context)
+    got = plugin.normalise_output(plugin.run_custom(runner, context))
+    if not plugin.uses_native_path(runner):
+        result["skipped"] = f"reference fallback ({getattr(runner, 'fallback_reason', 'reference path')})"
+        return result
+    got = got.reshape(want.shape).float()
+    diff = (got - want.float()).abs()
+    result["max_abs"] = float(diff.max())
+    result["within_tolerance"] = bool(torch.all(diff <= 3e-3 + 2e-2 * want.float().abs()).item())
+
+    def timed(fn):
+        for _ in range(10):
+            fn()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(calls):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) * 1e3 / calls
+
+    # reversed order on the second arm, as the reference alternates its arms
+    result["builtin_us_per_call"] = round(timed(lambda: plugin.run_custom(builtin, context)), 2)
+    result["custom_us_per_call"] = round(timed(lambda: plugin.run_custom(runner, context)), 2)
+    result["note"] = ("executor call (gate/up/SwiGLU/down + fused combine) of one token over its ten routed "
+                      "experts; host dispatch included in both arms")
+    return result
+
+
+def numpy_oracle_ms(spec, seed, tokens=4):
+    """The NumPy oracle's time per decode token at ``spec`` (one layer,
+    materialised experts), on this host."""
+    from oracle import moe_oracle as mo
+    from veymoe import synth
+
+    layer = synth.numpy_layer(spec, seed, 1, materialise=True)
+    xs = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
+    mo.moe_layer(xs[:1], layer, "bf16")
+    t0 = time.perf_counter()
+    for t in range(tokens):
+        mo.moe_layer(xs[t:t + 1], layer, "bf16")
+    return (time.perf_counter() - t0) * 1e3 / tokens
+
+
+KERNEL_FAMILIES = ("router", "gateup", "down")
+
+
+def main():
+    parser = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=400,
+                        help="timed steps; a step is one decode token through the --layers layer stack")
+    parser.add_argument("--warmup", type=int, default=40)
+    parser.add_argument("--layers", type=int, default=48)
+    parser.add_argument("--seed", type=int, default=2026)
+    parser.add_argument("--eager", action="store_true", help="launch layer by layer instead of graph replay")
+    parser.add_argument("--cpu-seconds", type=float, default=12.0)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-grouped", action="store_true",
+                        help="skip the batched (32 rows) and prefill (2048 rows) grouped workloads")
+    parser.add_argument("--no-stack", action="store_true",
+                        help="skip the 48-layer stack with the LRU pool and host-staged misses")
+    parser.add_argument("--no-small", action="store_true", help="skip the small decode layer (hidden 1024)")
+    parser.add_argument("--no-branch", action="store_true", help="skip the decoder MLP branch")
+    parser.add_argument("--custom-executor", "--executor", "--custom", dest="custom", default=None,
+                        help="module:attr of an executor to validate and time beside this package's "
+                             "(the reference harness's plug-in convention)")
+    parser.add_argument("--copy-probe-mib", type=int, default=0,
+                        help="after the timed work, stream this many MiB through one elementwise bf16 kernel "
+                             "(out = in * 1): the reference reading for HBM byte counters")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the MoE layer "
+              "path runs on one GPU, and sharding it across GPUs (by requests or layers for "
+              "decode, by experts with an all-to-all of the routed rows for prefill) is not "
+              "built", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 20:
+        log(f"note: {args.steps} timed steps ({args.steps * args.layers} layer-tokens)")
+
+    import torch
+
+    from veymoe import synth
+
+    spec = synth.CONFIGS["decode"]
+    layers = args.layers
+    timing, stack, pool, graph = run_decode(spec, layers, args.steps, args.warmup, args.seed, args.eager)
+    kernels, nbytes = timing["kernels"], timing["bytes"]
+    layer_s = timing["layer_s"]
+    roof_name = "gateup" if "gateup" in kernels else next(iter(kernels))
+    roof = kernels[roof_name]
+    roofline = {"bound": "hbm", "kernel": ROOFLINE_KERNEL.get(roof_name, roof_name),
+                "achieved": roof["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(roof["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic()}
     result = {
         "metric": "MoE-layer decode tok/s + achieved HBM GB/s (% peak); prefill tok/s at 2048",
-        "value": round(steps / elapsed, 1),
+        "value": round(1.0 / layer_s, 1),
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
-        "ms_per_step": round(ms_per_step, 5),
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(timing["elapsed_s"] * 1e3 / args.steps, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -563,19 +705,41 @@ def main():
         "data": "synthetic",
         "config": {"workload": "decode layer: hidden 2048, inter 512, 512 experts top-10 + shared (inter 512), "
                                "batch 1, Q4/G32 experts in an HBM pool behind an int32 slot table",
-                   "layers_cycled": layers, "pool_gb": round(pool.buffer.numel() / 1e9, 2),
-                   "launch": "hipgraph" if graph is not None else "eager",
+                   "step": f"one token through {layers} distinct layers (value counts layer-tokens)",
+                   "layers_cycled": layers, "pool_gb": timing["pool_gb"], "launch": timing["launch"],
                    "parallelism": "single GPU"},
+        "us_per_layer": round(layer_s * 1e6, 3),
         "layer_bytes": nbytes["layer"],
-        "layer_gbps": round(nbytes["layer"] / (ms_per_step * 1e6), 1),
-        "layer_frac_of_hbm_peak": round(nbytes["layer"] / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+        "layer_gbps": round(nbytes["layer"] / layer_s / 1e9, 1),
+        "layer_frac_of_hbm_peak": round(nbytes["layer"] / layer_s / 1e9 / HBM_PEAK_GBPS, 4),
+        "timed_wall_s": round(timing["wall_s"], 4),
         "kernels": kernels,
         "roofline": roofline,
     }
-    log("decoder MLP branch: hyper-connection + MoE layer + stream injection")
-    result["decoder_branch"] = run_branch(stack, spec, steps, warmup, args.seed, ms_per_step)
-    del graph, stack, pool, call_args, refs
+    if not args.no_branch:
+        log("decoder MLP branch: hyper-connection + MoE layer + stream injection")
+        result["decoder_branch"] = run_branch(stack, spec, args.steps, args.warmup, args.seed, layer_s * 1e3)
+    del graph, stack, pool
     torch.cuda.empty_cache()
+    if not args.no_small:
+        log("small decode layer (hidden 1024, inter 256, 64 experts top-4, no shared expert)")
+        small = synth.CONFIGS["decode_small"]
+        # 256 layers: the experts one pass touches (256 x 2.1 MB) exceed the 256 MB Infinity Cache
+        t_small, s_stack, s_pool, s_graph = run_decode(small, 256, max(20, args.steps // 4), 10, args.seed + 5)
+        b = algorithmic_bytes(small)
+        result["decode_small"] = {
+            "workload": "hidden 1024, inter 256, 64 experts top-4, no shared expert, batch 1, Q4/G32 pool",
+            "layers_cycled": 256, "us_per_layer": round(t_small["layer_s"] * 1e6, 3),
+            "tok_s": round(1.0 / t_small["layer_s"], 1), "layer_bytes": b["layer"],
+            "layer_gbps": round(b["layer"] / t_small["layer_s"] / 1e9, 1),
+            "layer_frac_of_hbm_peak": round(b["layer"] / t_small["layer_s"] / 1e9 / HBM_PEAK_GBPS, 4),
+            "kernels": t_small["kernels"],
+            "numpy_oracle_ms_per_token": round(numpy_oracle_ms(small, args.seed), 2)}
+        del s_stack, s_pool, s_graph
+        torch.cuda.empty_cache()
+    if args.custom:
+        log(f"custom executor {args.custom}")
+        result["custom_executor"] = run_custom_executor(args.custom, args.seed)
     if not args.no_grouped:
         log("batched decode: 32 rows, Zipf(1.1) routing")
         result["batched"] = run_grouped("batched", 32, 8, 50, args.seed)
@@ -592,6 +756,7 @@ def main():
                                  "device_lru_zipf_recipe": run_stack(args.seed, device_lru=True),
                                  "device_lru_hit_rate_60": run_stack(args.seed, bias_scale=0.45, device_lru=True)}
     if args.copy_probe_mib:
+        device = torch.device("cuda:0")
         n = args.copy_probe_mib * (1 << 20) // 2
         probe_in = torch.ones(n, dtype=torch.bfloat16, device=device)
         probe_out = torch.empty_like(probe_in)
@@ -605,6 +770,9 @@ def main():
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(spec, args.seed, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+ROOFLINE_KERNEL = {"gateup": "gateup (routed + shared gate/up Q4 GEMV + SwiGLU)"}
 
 
 if __name__ == "__main__":

@@ -210,8 +210,15 @@ typedef struct VmLayerArgs {
   const void* inject_weights;    /* [tokens, hc_count] */
   void* inject_out;              /* [tokens, hc_count * hidden] */
   uint32_t hc_count;
-  uint32_t reserved;
+  /* Decode calls (tokens <= VM_LAYER_MAX_TOKENS): VM_COMBINE_FUSED, or
+   * VM_COMBINE_GENERIC for the generic combine formula above.  The reference
+   * takes the generic one for layer 0 (metal_combines_scores is False there,
+   * expert_cache.py:1434-1443; adaptive_topk.py:271-278).  Grouped calls
+   * always combine generically. */
+  uint32_t combine;
 } VmLayerArgs;
+#define VM_COMBINE_FUSED 0u
+#define VM_COMBINE_GENERIC 1u
 #define VM_PHASE_ROUTER 1u
 #define VM_PHASE_EXPERTS 2u
 #define VM_MAX_STREAMS 8

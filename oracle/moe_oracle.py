@@ -363,17 +363,31 @@ def shared_expert(x, layer, mode, group_size=GROUP_SIZE, qmm=False):
     return shared, sigmoid(logit, mode)
 
 
-def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None):
+def decode_combine(layer_id):
+    """The combine a decode call (rows <= 8) of layer ``layer_id`` takes.
+
+    ``StreamingSwitchGLU.metal_combines_scores`` is False for layer 0
+    (expert_cache.py:1434-1443), so the reference's layer 0 decodes through
+    the generic combine of adaptive_topk.py:275-278 and every other layer
+    through the fused one (:289-293)."""
+    return "generic" if layer_id == 0 else "fused"
+
+
+def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None, combine=None):
     """One MoE layer.  ``layer`` holds numpy arrays (see veymoe.synth).
 
-    path "decode": rows <= 8, fused shared_y combine (adaptive_topk.py:289-293),
-    vector-form projections;
+    path "decode": rows <= 8, vector-form projections, and the combine of
+    ``decode_combine(layer["layer_id"])``: fused shared_y combine
+    (adaptive_topk.py:289-293), or the generic one for layer 0;
     path "prefill": generic combine (adaptive_topk.py:275-278), matrix-form
     projections (gather_qmm, weights rounded) unless ``qmm`` says otherwise.
+    ``combine`` ("fused"/"generic") overrides the rule.
     Returns dict(inds, scores, gates, output, down, shared, shared_gate)."""
     x = np.asarray(x, dtype=np.float32)
     if qmm is None:
         qmm = path != "decode"
+    if combine is None:
+        combine = decode_combine(layer.get("layer_id")) if path == "decode" else "generic"
     k = int(layer["top_k"])
     inds, scores, gates = route(x, layer["router"], k, mode, layer.get("router_bias"))
     shared, shared_gate = shared_expert(x, layer, mode, group_size, qmm)
@@ -390,7 +404,7 @@ def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None):
     shared_y = None
     if shared is not None:
         shared_y = _round(shared_gate * shared, mode)
-    if path == "decode":
+    if combine == "fused":
         out = fused_combine(down, scores, mode, shared_y=shared_y)
     else:
         out = generic_combine(down, scores, mode, shared_y)

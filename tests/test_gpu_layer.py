@@ -134,3 +134,44 @@ def test_pool_misses_are_staged_and_match_the_dense_layer(device):
     sw = pooled.switch_mlp
     assert sw.misses > 0 and pool.bytes_staged == sw.misses * layout.record_bytes
     assert pool.usable_slots == 16
+
+
+def test_layer_zero_combines_generically_and_later_layers_fuse(device):
+    """The reference's layer 0 is not on the custom path
+    (metal_combines_scores is False for layer_id 0, expert_cache.py:1434-1443),
+    so its decode output is ``(y * scores[..., None]).sum(-2)`` with
+    elementwise bf16 products (adaptive_topk.py:275-278); later layers take
+    the fused combine.  Same weights and input in both: each output equals its
+    formula applied, in fp32 with bf16 roundings, to the per-slot expert
+    outputs of the same kernels, bit for bit."""
+    from veymoe.layer import HipSwitchGLU, MoELayer
+
+    spec = synth.CONFIGS["decode_small"]
+    seed = 211
+    l0 = assemble.build_layer(spec, seed, device, dense=True)
+    sw = l0.switch_mlp
+    sw1 = HipSwitchGLU(sw.hidden, sw.inter, sw.num_experts, layer_id=1,
+                       projections={"gate_proj": sw.gate_proj, "up_proj": sw.up_proj, "down_proj": sw.down_proj})
+    l1 = MoELayer(l0.gate, sw1, l0.top_k)
+    assert not sw.metal_combines_scores and sw1.metal_combines_scores
+    x = assemble.tokens_tensor(spec, seed, device, 3, stream=5)
+    y0 = l0(x[None])[0]
+    inds0, scores0 = l0.last_inds.clone(), l0.last_scores.clone()
+    y1 = l1(x[None])[0]
+    assert torch.equal(inds0, l1.last_inds) and torch.equal(scores0, l1.last_scores)
+    # per-slot outputs: the custom path is not taken for layer 0 even with scores
+    per_slot = sw(x[:, None, :], inds0[:, None, :], scores=scores0[:, None, :])[:, 0]
+    assert per_slot.shape == (3, spec.top_k, spec.hidden) and not sw._last_fused_shared
+    d = host(per_slot)
+    s = host(scores0)
+    fused = np.zeros((3, spec.hidden), np.float32)
+    generic = np.zeros_like(fused)
+    for j in range(spec.top_k):
+        fused = (fused + d[:, j] * s[:, j:j + 1]).astype(np.float32)
+        generic = (generic + mo.bf16r(d[:, j] * s[:, j:j + 1])).astype(np.float32)
+    np.testing.assert_array_equal(host(y1), mo.bf16r(fused))
+    np.testing.assert_array_equal(host(y0), mo.bf16r(generic))
+    assert not np.array_equal(host(y0), host(y1))
+    ref = mo.moe_layer(mo.bf16_bits_to_f32(synth.tokens(spec, seed, 3, stream=5)), synth.numpy_layer(spec, seed),
+                       "bf16")
+    assert_close(host(y0), ref["output"], "layer 0 decode output, generic combine")

@@ -1,0 +1,174 @@
+"""The 48-layer stack's LRU pool at full size on the GPU.
+
+A pool of 3,051 slots (= (6e9 - 4096) // 1,966,080, expert_pool.py:92) of
+hidden 2048 / inter 512 records in front of several full-width layers
+(512 experts, top-10, shared expert).  3,051 queue entries over the
+1024-thread assign block run the 4-entries-per-thread instance of the device
+LRU.  The pool is warmed by the host LRU with more (layer, expert) keys than
+it holds, so the device starts with a full queue and evicts from the first
+call.
+
+Checked after every call or replay, against ``oracle.pool_oracle.LruSlots``
+(expert_pool.py:123-159) fed the same routed ids:
+
+* device LRU calls and StepGraph replays give the resident reference layers'
+  outputs bit for bit;
+* slot table, owners and queue equal the reference's table, owners and
+  free list + OrderedDict order;
+* a host-LRU pool of the same size fed the same tokens gives the same outputs
+  and ends in the same state;
+* every resident record equals its host record byte for byte.
+
+Records: 64 distinct full-size records in pinned memory, aliased over every
+(layer, expert) id (row = (layer * 512 + expert) % 64), as the bench's stack
+does; the reference layers read the same 64 records through a 64-slot pool
+whose slot tables map every expert to its record."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pool_oracle
+from veymoe import assemble, synth
+from veymoe.graph import StepGraph
+from veymoe.layer import HipSwitchGLU, MoELayer, QuantizedMLP, RouterLinear
+from veymoe.pool import ExpertPool, HostRecordStore
+
+pytestmark = pytest.mark.gpu
+
+SPEC = synth.LayerSpec("stack_full", 2048, 512, 512, 10, 512, 1)
+SEED = 48
+LAYERS = 7
+SLOTS = (6_000_000_000 - 4096) // SPEC.layout.record_stride
+DISTINCT = 64
+
+
+def _row(layer, expert):
+    return (layer * SPEC.experts + expert) % DISTINCT
+
+
+def _store():
+    store = HostRecordStore(SPEC.layout, DISTINCT)
+    for r in range(DISTINCT):
+        store.put(0, r, synth.expert_record(SPEC, SEED, 0, r))
+    for layer in range(LAYERS):
+        for e in range(SPEC.experts):
+            store.alias(layer, e, _row(layer, e))
+    return store
+
+
+def _layer(layer, pool, device, store=None):
+    np_layer = synth.numpy_layer(SPEC, SEED, layer)
+    gate = RouterLinear(assemble.bf16_tensor(np_layer["router"], device))
+    shared = QuantizedMLP(*(assemble.projection(*np_layer[n], device)
+                            for n in ("shared_gate_proj", "shared_up_proj", "shared_down_proj")))
+    switch = HipSwitchGLU(SPEC.hidden, SPEC.inter, SPEC.experts, pool=pool, layer_id=layer, host_store=store)
+    return MoELayer(gate, switch, SPEC.top_k, shared_expert=shared,
+                    shared_expert_gate=assemble.projection(*np_layer["shared_expert_gate"], device))
+
+
+def _reference_layers(store, device):
+    pool = ExpertPool(SPEC.layout, DISTINCT, layers=LAYERS, experts=SPEC.experts, device=device)
+    for r in range(DISTINCT):
+        pool.record(r).copy_(store.buffer[r].to(device))
+    for layer in range(LAYERS):
+        pool._host_table[layer] = [_row(layer, e) for e in range(SPEC.experts)]
+        pool._dirty.add(layer)
+    pool.sync_tables()
+    return pool, [_layer(l, pool, device) for l in range(LAYERS)]
+
+
+def _warm(pool, ref, store):
+    """Host LRU over every key of every layer in a shuffled order: more keys
+    than slots, so the queue ends full with evictions behind it."""
+    rng = np.random.default_rng(SEED)
+    for layer in rng.permutation(LAYERS):
+        experts = [int(e) for e in rng.permutation(SPEC.experts)]
+        for i in range(0, len(experts), 64):
+            _, misses = pool.assign(int(layer), experts[i:i + 64])
+            assert misses == ref.assign(int(layer), experts[i:i + 64])[1]
+            pool.fill(int(layer), misses, store)
+    pool.sync_tables()
+
+
+def _expected_table(ref):
+    table = np.full((LAYERS, SPEC.experts), -1, np.int32)
+    for (layer, expert), slot in ref.slot_of.items():
+        table[layer, expert] = slot
+    return table
+
+
+def _check_state(lru, ref, where):
+    table, owner, order = lru.state()
+    np.testing.assert_array_equal(table, _expected_table(ref), err_msg=where)
+    want_owner = np.full(SLOTS, -1, np.int32)
+    for (layer, expert), slot in ref.slot_of.items():
+        want_owner[slot] = layer * SPEC.experts + expert
+    np.testing.assert_array_equal(owner, want_owner, err_msg=where)
+    assert order.tolist() == list(reversed(ref.free)) + list(ref.slot_of.values()), where
+
+
+def _check_records(pool, store, ref, device):
+    nbytes = SPEC.layout.record_bytes
+    rows = store.buffer[:, :nbytes].to(device)
+    for (layer, expert), slot in ref.slot_of.items():
+        assert torch.equal(pool.record(slot)[:nbytes], rows[_row(layer, expert)]), (layer, expert, slot)
+
+
+def _tokens(step, rows, device):
+    return torch.stack([assemble.tokens_tensor(SPEC, SEED, device, rows, stream=100 * step + l)
+                        for l in range(LAYERS)])
+
+
+def test_full_size_pool_of_3051_slots_device_lru_graph_and_host_lru(device):
+    assert SLOTS == 3051 and SLOTS > 2048          # more than two queue entries per assign thread
+    store = _store()
+    ref_pool, reference = _reference_layers(store, device)
+    dev_pool = ExpertPool(SPEC.layout, SLOTS, layers=LAYERS, experts=SPEC.experts, device=device)
+    host_pool = ExpertPool(SPEC.layout, SLOTS, layers=LAYERS, experts=SPEC.experts, device=device)
+    ref = pool_oracle.LruSlots(SLOTS)
+    host_ref = pool_oracle.LruSlots(SLOTS)
+    _warm(dev_pool, ref, store)
+    _warm(host_pool, host_ref, store)
+    assert ref.misses > SLOTS
+    device_layers = [_layer(l, dev_pool, device, store) for l in range(LAYERS)]
+    host_layers = [_layer(l, host_pool, device, store) for l in range(LAYERS)]
+    lru = dev_pool.attach_device_lru(store)
+    assert lru.order_len == SLOTS
+    warm_hits, warm_misses = ref.hits, ref.misses
+
+    def check_outputs(step, rows, out, x):
+        for l in range(LAYERS):
+            want = reference[l](x[l][None])[0]
+            got_host = host_layers[l](x[l][None])[0]
+            torch.cuda.synchronize()
+            assert torch.equal(out[l].view(torch.int16), want.view(torch.int16)), (step, rows, l)
+            assert torch.equal(got_host.view(torch.int16), want.view(torch.int16)), (step, rows, l)
+            routed = reference[l].last_inds.cpu().numpy().reshape(-1).tolist()
+            ref.assign(l, routed)
+            host_ref.assign(l, routed)
+
+    # eager device-LRU calls, one and two tokens
+    for step in range(6):
+        rows = 1 + step % 2
+        x = _tokens(step, rows, device)
+        out = torch.stack([device_layers[l](x[l][None])[0] for l in range(LAYERS)])
+        check_outputs(step, rows, out, x)
+        _check_state(lru, ref, f"eager step {step}")
+    # the same layers replayed as one graph per step
+    graph = StepGraph(device_layers, rows=1, device=device).capture()
+    for step in range(6, 14):
+        x = _tokens(step, 1, device)
+        out = graph.replay(x).clone()
+        torch.cuda.synchronize()
+        check_outputs(step, 1, out, x)
+        _check_state(lru, ref, f"replay step {step}")
+    stats = lru.stats()
+    assert (stats["hits"], stats["misses"]) == (ref.hits - warm_hits, ref.misses - warm_misses)
+    assert stats["misses"] > 0
+    assert list(host_pool._slot_of.items()) == list(host_ref.slot_of.items())
+    assert host_pool._free == host_ref.free
+    assert list(host_ref.slot_of.items()) == list(ref.slot_of.items())
+    _check_records(dev_pool, store, ref, device)
+    _check_records(host_pool, store, host_ref, device)
+    print(f"[stack] {SLOTS} slots, {LAYERS} layers: device misses {stats['misses']}, hits {stats['hits']}")
+    del graph

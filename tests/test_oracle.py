@@ -260,17 +260,29 @@ def test_layer_modes_agree_within_bf16_tolerance():
 
 
 def test_layer_decode_is_composition_of_parts():
+    """Past layer 0 a decode layer is the fused executor call; layer 0 is the
+    per-slot expert outputs through the generic combine (expert_cache.py:1434-1443)."""
     from veymoe import synth
 
     spec = synth.LayerSpec("t", 128, 64, 16, 4, 64, 2)
     x = mo.bf16_bits_to_f32(synth.tokens(spec, 8))
-    layer = synth.numpy_layer(spec, 8)
-    out = mo.moe_layer(x, layer, "bf16")
-    inds, scores, _ = mo.route(x, layer["router"], 4, "bf16")
-    projections = {n: layer[n] for n in ("gate_proj", "up_proj", "down_proj")}
-    shared, sg = mo.shared_expert(x, layer, "bf16")
-    *_, fused = mo.execute(x, inds, projections, "bf16", scores=scores, shared_y=mo.bf16r(sg * shared))
-    np.testing.assert_array_equal(out["output"], fused)
+    for layer_id in (1, 0):
+        layer = synth.numpy_layer(spec, 8, layer_id)
+        out = mo.moe_layer(x, layer, "bf16")
+        inds, scores, _ = mo.route(x, layer["router"], 4, "bf16")
+        projections = {n: layer[n] for n in ("gate_proj", "up_proj", "down_proj")}
+        shared, sg = mo.shared_expert(x, layer, "bf16")
+        shared_y = mo.bf16r(sg * shared)
+        if layer_id:
+            *_, fused = mo.execute(x, inds, projections, "bf16", scores=scores, shared_y=shared_y)
+            np.testing.assert_array_equal(out["output"], fused)
+        else:
+            *_, down, _ = mo.execute(x, inds, projections, "bf16")
+            # (y * scores[..., None]).sum(-2) + shared, elementwise bf16 products
+            want = mo.bf16r(mo.bf16r(sum(mo.bf16r(down[:, j] * scores[:, j:j + 1]) for j in range(4)))
+                            + shared_y)
+            np.testing.assert_array_equal(out["output"], want)
+            assert not np.array_equal(out["output"], mo.moe_layer(x, layer, "bf16", combine="fused")["output"])
 
 
 def test_qmm_projection_matches_loops():

@@ -444,6 +444,8 @@ static int validate_layer(const VmLayerArgs* a) {
   if (rc != VM_OK) return rc;
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   if (phases & ~(VM_PHASE_ROUTER | VM_PHASE_EXPERTS)) return fail(VM_EINVAL, "unknown phase bits");
+  if (a->combine != VM_COMBINE_FUSED && a->combine != VM_COMBINE_GENERIC)
+    return fail(VM_EINVAL, "combine must be VM_COMBINE_FUSED or VM_COMBINE_GENERIC");
   if (a->inject_out != nullptr) {
     if (a->inject_hidden == nullptr || a->inject_weights == nullptr)
       return fail(VM_EINVAL, "an injection needs inject_hidden and inject_weights");
@@ -591,6 +593,7 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   d.score_dtype = static_cast<int>(a->act_dtype);
   d.out = a->output;
   d.inject = to_inject(a);
+  d.generic = a->combine == VM_COMBINE_GENERIC ? 1u : 0u;
   d.status = a->status;
   d.tokens = T;
   d.slots = K;

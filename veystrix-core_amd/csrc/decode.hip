@@ -945,8 +945,13 @@ __global__ __launch_bounds__(kDownBlock) void k_down(DownLaunch p) {
     if (tid < RB && row0 + tid < H) {
       const uint32_t r = tid;
       float combined = 0.0f;
-      for (uint32_t k = 0; k < K; ++k)
-        combined = __fadd_rn(combined, __fmul_rn(A::round(s_part[k * RB + r]), s_scores[k]));
+      if (p.generic) {
+        for (uint32_t k = 0; k < K; ++k)
+          combined = __fadd_rn(combined, A::round(__fmul_rn(A::round(s_part[k * RB + r]), s_scores[k])));
+      } else {
+        for (uint32_t k = 0; k < K; ++k)
+          combined = __fadd_rn(combined, __fmul_rn(A::round(s_part[k * RB + r]), s_scores[k]));
+      }
       float y = A::round(combined);
       if (p.has_shared) {
         const float sh = A::round(s_part[K * RB + r]);

@@ -93,6 +93,7 @@ struct DownLaunch {
   // Last, so that the fields above keep the kernel-argument offsets the
   // kernel's scalar loads are scheduled around.
   Inject inject;               // optional injection of the combined rows into residual streams
+  uint32_t generic;            // 1: generic combine (products rounded before the slot sum)
 };
 
 // ------------------------------------------------------ device-side LRU --

@@ -110,10 +110,12 @@ class VmLayerArgs(ctypes.Structure):
         ("inject_weights", _vp),
         ("inject_out", _vp),
         ("hc_count", _c_u32),
-        ("reserved", _c_u32),
+        ("combine", _c_u32),
     ]
 
 
+VM_COMBINE_FUSED = 0
+VM_COMBINE_GENERIC = 1
 VM_PHASE_ROUTER = 1
 VM_PHASE_EXPERTS = 2
 VM_MAX_STREAMS = 8

@@ -88,8 +88,10 @@ class HipSwitchGLU:
     @property
     def metal_combines_scores(self) -> bool:
         """Name kept from the reference: the patched MoE block asks it whether the
-        expert block combines scores itself (expert_cache.py:1434-1443)."""
-        return True
+        expert block combines scores itself (expert_cache.py:1434-1443).  As
+        there, layer 0 does not: its decode rows go through the generic combine
+        ``(y * scores[..., None]).sum(-2) + shared`` (adaptive_topk.py:271-278)."""
+        return self.layer_id > 0
 
     def executor(self, top_k: int) -> HipMoEExecutor:
         if self._executor is None or self._executor.top_k != top_k:
@@ -98,8 +100,15 @@ class HipSwitchGLU:
 
     # ------------------------------------------------------------- pool ---
     def _pool_fully_resident(self) -> bool:
-        table = self.pool._host_table[self.layer_id]
-        return bool((table >= 0).all())
+        """True when no call can change the pool's LRU state in a way that
+        matters: every expert of this layer is resident and the pool holds
+        every key of every layer, so nothing is ever evicted.  Otherwise a
+        call must make the host LRU pass even when all its experts hit, since
+        the reference moves hits to the most recent end (expert_pool.py:
+        139-144) and that order decides later evictions."""
+        pool = self.pool
+        table = pool._host_table[self.layer_id]
+        return bool((table >= 0).all()) and pool.holds_every_key()
 
     def resolve_routes(self, routed) -> np.ndarray:
         """Host LRU pass for a pool-backed layer: assign, stage misses, and
@@ -128,6 +137,13 @@ class HipSwitchGLU:
         k = int(indices.shape[-1])
         flat_inds = indices.reshape(-1, k).to(torch.int32).contiguous()
         rows = flat.shape[0]
+        if rows > MAX_DECODE_ROWS and flat.dtype == torch.bfloat16:
+            # the reference's rows > 8 path: per-slot expert outputs
+            # (expert_cache.py:1949-2037).  grouped_experts makes the call's
+            # only LRU pass over a pool, so hits and misses count once.
+            from .grouped import grouped_experts
+
+            return grouped_experts(self, flat, flat_inds).reshape(*x.shape[:-1], k, hidden)
         executor = self.executor(k)
         executor.max_tokens = max(executor.max_tokens, 1)
         if self.pool is not None:
@@ -140,12 +156,9 @@ class HipSwitchGLU:
             routes = flat_inds
             projections = (self.gate_proj, self.up_proj, self.down_proj)
             slab = None
-        if rows > MAX_DECODE_ROWS and flat.dtype == torch.bfloat16:
-            # the reference's rows > 8 path: per-slot expert outputs (expert_cache.py:1949-2037)
-            from .grouped import grouped_experts
-
-            return grouped_experts(self, flat, flat_inds).reshape(*x.shape[:-1], k, hidden)
-        combine = scores is not None and rows <= MAX_DECODE_ROWS
+        # the custom (combining) path only where the reference takes it:
+        # scores given, rows <= 8 and metal_combines_scores (expert_cache.py:1763-1767)
+        combine = scores is not None and rows <= MAX_DECODE_ROWS and self.metal_combines_scores
         if combine:
             out = executor._run(flat, routes, *projections, self.inter, False,
                                 scores.reshape(rows, k).contiguous(), slab, None,
@@ -243,6 +256,8 @@ class MoELayer:
         a.expert_count, a.top_k, a.group_size = sw.num_experts, self.top_k, sw.group_size
         a.act_dtype = dtype
         a.renorm_blend = self.renorm_blend
+        # layer 0 combines like the reference's generic path (expert_cache.py:1434-1443)
+        a.combine = _lib.VM_COMBINE_FUSED if sw.metal_combines_scores else _lib.VM_COMBINE_GENERIC
         return a
 
     def forward(self, flat: torch.Tensor, inject=None) -> torch.Tensor:

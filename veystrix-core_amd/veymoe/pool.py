@@ -173,6 +173,12 @@ class ExpertPool:
     def resident(self, layer: int, expert: int) -> bool:
         return (layer, expert) in self._slot_of
 
+    def holds_every_key(self) -> bool:
+        """Every (layer, expert) of the pool's table is mapped: no assign can
+        miss, so none evicts.  Mappings written straight into the host table
+        (static setups that share records between experts) count as well."""
+        return len(self._slot_of) == self.layers * self.experts or bool((self._host_table >= 0).all())
+
     # ---------------------------------------------------------- device ---
     def view(self) -> _lib.VmPoolView:
         view = _lib.VmPoolView()

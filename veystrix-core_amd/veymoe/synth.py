@@ -155,9 +155,9 @@ def slot_permutation(spec: LayerSpec, seed: int, slots: int) -> np.ndarray:
 def numpy_layer(spec: LayerSpec, seed: int, layer: int = 0, materialise: bool = False):
     """Layer dict in the form the oracle reads: ``gate_proj/up_proj/down_proj`` as
     (weight, scales, biases) indexable by expert, ``router``, ``router_bias``,
-    shared parts and ``top_k``.  Experts are generated lazily unless
-    ``materialise``."""
-    layer_dict = {"top_k": spec.top_k, "router": router_weight(spec, seed, layer),
+    shared parts, ``top_k`` and ``layer_id``.  Experts are generated lazily
+    unless ``materialise``."""
+    layer_dict = {"top_k": spec.top_k, "layer_id": int(layer), "router": router_weight(spec, seed, layer),
                   "router_bias": router_bias(spec, seed, layer)}
     for proj in ("gate_proj", "up_proj", "down_proj"):
         if materialise:
