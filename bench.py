@@ -111,7 +111,14 @@ def algorithmic_bytes(spec):
     slots = spec.top_k + (1 if spec.shared_inter else 0)
     gateup = slots * 2 * proj + spec.hidden * 2 + slots * spec.inter * 2
     down = slots * proj + slots * spec.inter * 2 + spec.hidden * 2
-    return {"layer": layer, "gateup": gateup, "down": down, "router": router + spec.hidden * 2}
+    # two-launch pipeline: the front also runs the shared expert's gate/up;
+    # the experts grid the routed gate/up and every slot's down rows
+    sh_gateup = 2 * proj if spec.shared_inter else 0
+    front = router + spec.hidden * 2 + seg + sh_gateup + spec.experts * 4
+    experts = (spec.top_k * 2 + slots) * proj + spec.experts * 4 + spec.hidden * 2 * 2 + spec.shared_inter * 2
+    gateup_routed = spec.top_k * 2 * proj + spec.experts * 4 + spec.hidden * 2 + spec.top_k * spec.inter * 2
+    return {"layer": layer, "gateup": gateup, "down": down, "router": router + spec.hidden * 2,
+            "front": front, "experts": experts, "gateup_routed": gateup_routed}
 
 
 def cpu_baseline(spec, seed, seconds):
@@ -168,14 +175,16 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0
 TRAFFIC_SUMMARY = os.path.join(ROOT, "profiles", "hbm_traffic_decode_grouped_pmc.md")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the decode gate/up kernel from the committed
+def measured_traffic(kernel):
+    """HBM bytes per launch of a decode kernel family from the committed
     rocprofv3 FETCH_SIZE/WRITE_SIZE summary (counters scaled by a copy kernel
-    of known size), or None when the summary is absent."""
+    of known size): its line ``traffic_bytes_per_launch[<kernel>]: N``, or
+    None when the summary has none for it."""
+    key = f"traffic_bytes_per_launch[{kernel}]:"
     try:
         with open(TRAFFIC_SUMMARY) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key):
                     return int(line.split(":", 1)[1])
     except (OSError, ValueError):
         return None
@@ -544,10 +553,16 @@ def run_decode(spec, layers, steps, warmup, seed, eager=False):
         if launches.value:
             kernels[name] = {"avg_us": round(total.value * 1e3 / launches.value, 3), "launches": int(launches.value)}
     nbytes = algorithmic_bytes(spec)
+    one_token = lib.vm_decode_pipeline(-1) != 0
     for name in kernels:
-        if name in nbytes:
-            kernels[name]["bytes"] = nbytes[name]
-            kernels[name]["gbps"] = round(nbytes[name] / (kernels[name]["avg_us"] * 1e3), 1)
+        key = name
+        if one_token and name == "router":
+            key = "front"
+        elif one_token and name == "gateup":
+            key = "gateup_routed"
+        if key in nbytes:
+            kernels[name]["bytes"] = nbytes[key]
+            kernels[name]["gbps"] = round(nbytes[key] / (kernels[name]["avg_us"] * 1e3), 1)
     layer_s = elapsed / (steps * layers)
     timing = {"elapsed_s": elapsed, "wall_s": wall, "layer_s": layer_s, "launch": "hipgraph" if graph else "eager",
               "pool_gb": round(pool.buffer.numel() / 1e9, 2), "kernels": kernels, "bytes": nbytes}
@@ -637,7 +652,7 @@ def numpy_oracle_ms(spec, seed, tokens=4):
     return (time.perf_counter() - t0) * 1e3 / tokens
 
 
-KERNEL_FAMILIES = ("router", "gateup", "down")
+KERNEL_FAMILIES = ("router", "experts", "gateup", "down")
 
 
 def main():
@@ -649,6 +664,10 @@ def main():
     parser.add_argument("--layers", type=int, default=48)
     parser.add_argument("--seed", type=int, default=2026)
     parser.add_argument("--eager", action="store_true", help="launch layer by layer instead of graph replay")
+    parser.add_argument("--pipeline", type=int, default=0, choices=(0, 1, 2),
+                        help="one-token decode kernels (vm_decode_pipeline): 0 router, gate/up, down (default); "
+                             "1 front with the shared expert + gate/up grid + down; 2 front + experts grid with "
+                             "the tagged hand-off")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-grouped", action="store_true",
@@ -682,14 +701,16 @@ def main():
 
     spec = synth.CONFIGS["decode"]
     layers = args.layers
+    from veymoe import _lib
+    _lib.lib().vm_decode_pipeline(args.pipeline)
     timing, stack, pool, graph = run_decode(spec, layers, args.steps, args.warmup, args.seed, args.eager)
     kernels, nbytes = timing["kernels"], timing["bytes"]
     layer_s = timing["layer_s"]
-    roof_name = "gateup" if "gateup" in kernels else next(iter(kernels))
+    roof_name = "experts" if "experts" in kernels else "gateup" if "gateup" in kernels else next(iter(kernels))
     roof = kernels[roof_name]
     roofline = {"bound": "hbm", "kernel": ROOFLINE_KERNEL.get(roof_name, roof_name),
                 "achieved": roof["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(roof["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic()}
+                "frac": round(roof["gbps"] / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(roof_name)}
     result = {
         "metric": "MoE-layer decode tok/s + achieved HBM GB/s (% peak); prefill tok/s at 2048",
         "value": round(1.0 / layer_s, 1),
@@ -707,6 +728,7 @@ def main():
                                "batch 1, Q4/G32 experts in an HBM pool behind an int32 slot table",
                    "step": f"one token through {layers} distinct layers (value counts layer-tokens)",
                    "layers_cycled": layers, "pool_gb": timing["pool_gb"], "launch": timing["launch"],
+                   "pipeline": args.pipeline,
                    "parallelism": "single GPU"},
         "us_per_layer": round(layer_s * 1e6, 3),
         "layer_bytes": nbytes["layer"],
@@ -772,7 +794,8 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-ROOFLINE_KERNEL = {"gateup": "gateup (routed + shared gate/up Q4 GEMV + SwiGLU)"}
+ROOFLINE_KERNEL = {"gateup": "gateup (gate/up Q4 GEMV + SwiGLU)",
+                   "experts": "experts grid (routed gate/up + SwiGLU, every slot's down rows, combine)"}
 
 
 if __name__ == "__main__":

@@ -387,11 +387,25 @@ int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride,
                   const int64_t* src_index, const int64_t* dst_slot, uint32_t count,
                   void* stream);
 
+/* vm_decode_pipeline: the kernels of one-token bf16 decode calls (vm_moe_layer
+ * and vm_moe_layer_lru), process-wide:
+ *   0 (the default): the multi-token kernels (router, gate/up with the
+ *     shared expert, down);
+ *   1: the one-token front (router logits, the shared expert's gate/up and
+ *     its sigmoid gate), a gate/up grid of one block per CU over the routed
+ *     experts, and the down + combine kernel;
+ *   2: two launches, the front and one experts grid that hands its gate/up
+ *     activations to its down rows through tagged words.
+ * All three give the same bits.  -1 queries.  Returns the previous setting.
+ * No counterpart in the reference: it is for A/B measurement and the parity
+ * tests of the pipelines. */
+int vm_decode_pipeline(int mode);
+
 /* Per-kernel event timing over a window of calls (for rooflines).  While
  * enabled, every kernel the library launches is bracketed by hipEvents on its
  * stream; vm_timing_read returns the summed milliseconds and launch count of
- * the kernel family `name` ("router", "gateup", "down", "grouped_gateup",
- * "grouped_down", "sort", "combine"). */
+ * the kernel family `name` ("router", "gateup", "down", "experts",
+ * "grouped_gateup", "grouped_down", "sort", "combine"). */
 int vm_timing_enable(int enabled);
 int vm_timing_read(const char* name, double* total_ms, uint64_t* launches);
 int vm_timing_reset(void);

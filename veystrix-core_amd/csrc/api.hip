@@ -6,6 +6,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -343,7 +345,7 @@ int vm_router_topk(const VmRouterArgs* a, void* stream_ptr) {
 //            [fill list of the device LRU: count, source rows, slots]
 
 struct LayerWs {
-  uint64_t logits, act, sig, inds, scores, words, fill, total;
+  uint64_t logits, act, sig, inds, scores, words, fill, tags, total;
 };
 
 static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_t E, uint32_t dtype) {
@@ -356,8 +358,93 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   w.scores = w.inds + align_up(uint64_t(T) * K * 4);
   w.words = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
   w.fill = w.words + align_up(uint64_t(T) * K * 4);
-  w.total = w.fill + align_up(4 + 8 * uint64_t(vm::kLruMaxRouted));
+  w.tags = w.fill + align_up(4 + 8 * uint64_t(vm::kLruMaxRouted));
+  w.total = w.tags + align_up(vm::tag_words(K * I) * 4);   // hand-off words of the one-token pipeline
   return w;
+}
+
+// -------------------------------------------------------- fused decode ---
+// The decode pipeline of one-token calls, process-wide:
+//   0  k_front, k_gateup (routed + shared pairs), k_down (the default: the
+//      fastest measured, 14.6 us per layer against 16.1 and 21.4 at hidden
+//      2048 / inter 512 / 512 experts top-10 + shared);
+//   1  the one-token front (router + shared expert gate/up), the gate/up grid
+//      of a block per CU, k_down;
+//   2  the one-token front and the experts grid with the tagged hand-off.
+static std::atomic<int> g_fused_decode{0};
+
+// Compute units of the current device: the experts grid is one block per CU
+// so that all of it is resident at once.
+static uint32_t device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 0;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return static_cast<uint32_t>(v);
+}
+
+static vm::Inject to_inject(const VmLayerArgs* a) {
+  vm::Inject j{};
+  if (a->inject_out != nullptr) {
+    j.hidden = a->inject_hidden;
+    j.weights = a->inject_weights;
+    j.out = a->inject_out;
+    j.hc = a->hc_count;
+  }
+  return j;
+}
+
+// The fused launch arguments of a one-token bf16 call, or false when the
+// three-launch path serves it.
+static bool fused_args(const VmLayerArgs* a, const LayerWs& w, char* ws, vm::FusedLaunch& f, uint32_t& blocks,
+                       bool& two_launch) {
+  const int mode = g_fused_decode.load(std::memory_order_relaxed);
+  if (mode == 0) return false;
+  two_launch = mode == 2;
+  if (a->tokens != 1 || a->act_dtype != VM_BF16) return false;
+  blocks = device_cus();
+  const uint32_t K = a->top_k, I = a->inter_size, H = a->hidden_size;
+  const bool shared = a->shared_inter != 0;
+  f = vm::FusedLaunch{};
+  if (!vm::fused_plan(H, I, K, shared ? 1u : 0u, a->expert_count, blocks, f)) return false;
+  f.x = static_cast<const uint16_t*>(a->x);
+  f.router = a->router_weight;
+  f.router_bias = a->router_bias;
+  f.logits = reinterpret_cast<float*>(ws + w.logits);
+  if (shared) {
+    f.sh_gate = to_ptrs(a->shared_gate_proj);
+    f.sh_up = to_ptrs(a->shared_up_proj);
+    f.sh_down = to_ptrs(a->shared_down_proj);
+    f.sh_seg = to_ptrs(a->shared_expert_gate);
+  }
+  // activations [K + 1, I]: routed slots, then the shared expert's
+  f.act = reinterpret_cast<uint16_t*>(ws + w.act);
+  f.sh_act = f.act + uint64_t(K) * I;
+  f.sh_sig = reinterpret_cast<uint16_t*>(ws + w.sig);
+  f.slot_table = a->slot_table;
+  f.pool = to_pool(a->pool);
+  f.gate = to_ptrs(a->gate);
+  f.up = to_ptrs(a->up);
+  f.down = to_ptrs(a->down);
+  f.act_tag = two_launch ? reinterpret_cast<uint32_t*>(ws + w.tags) : nullptr;
+  f.words_out = reinterpret_cast<uint32_t*>(ws + w.words);
+  f.out = static_cast<uint16_t*>(a->output);
+  f.inds_out = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
+  f.scores_out = static_cast<uint16_t*>(a->scores_out != nullptr ? a->scores_out : static_cast<void*>(ws + w.scores));
+  f.status = a->status;
+  f.inject = to_inject(a);
+  f.hidden = H;
+  f.inter = I;
+  f.experts = a->expert_count;
+  f.slots = K;
+  f.has_shared = shared ? 1u : 0u;
+  f.generic = a->combine == VM_COMBINE_GENERIC ? 1u : 0u;
+  f.blend = a->renorm_blend;
+  return true;
 }
 
 // Workspace of the grouped path (more than VM_LAYER_MAX_TOKENS rows).
@@ -457,17 +544,6 @@ static int validate_layer(const VmLayerArgs* a) {
   return VM_OK;
 }
 
-static vm::Inject to_inject(const VmLayerArgs* a) {
-  vm::Inject j{};
-  if (a->inject_out != nullptr) {
-    j.hidden = a->inject_hidden;
-    j.weights = a->inject_weights;
-    j.out = a->inject_out;
-    j.hc = a->hc_count;
-  }
-  return j;
-}
-
 int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   int rc = validate_layer(a);
   if (rc != VM_OK) return rc;
@@ -514,6 +590,35 @@ static hipError_t launch_layer_front(const VmLayerArgs* a, const LayerWs& w, cha
   return vm::launch_front(f, stream);
 }
 
+// The down + combine launch of a decode call: activations [T, S, I] in the
+// workspace, routes as route words (slot_table null) or expert ids.
+static vm::DownLaunch down_args(const VmLayerArgs* a, const LayerWs& w, char* ws, const uint32_t* routes,
+                                const int32_t* slot_table, void* scores) {
+  const bool shared = a->shared_inter != 0;
+  vm::DownLaunch d{};
+  d.act = ws + w.act;
+  d.routes = routes;
+  d.slot_table = slot_table;
+  d.down = to_ptrs(a->down);
+  if (shared) d.shared_down = to_ptrs(a->shared_down_proj);
+  d.shared_sig = ws + w.sig;
+  d.pool = to_pool(a->pool);
+  d.scores = scores;
+  d.score_dtype = static_cast<int>(a->act_dtype);
+  d.out = a->output;
+  d.inject = to_inject(a);
+  d.generic = a->combine == VM_COMBINE_GENERIC ? 1u : 0u;
+  d.status = a->status;
+  d.tokens = a->tokens;
+  d.slots = a->top_k;
+  d.hidden = a->hidden_size;
+  d.inter = a->inter_size;
+  d.experts = a->expert_count;
+  d.has_shared = shared ? 1 : 0;
+  d.act_dtype = static_cast<int>(a->act_dtype);
+  return d;
+}
+
 static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   const uint32_t T = a->tokens, K = a->top_k, H = a->hidden_size, I = a->inter_size, E = a->expert_count;
   const bool shared = a->shared_inter != 0;
@@ -533,6 +638,19 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   // split: a select kernel publishes inds/scores for the host between phases
   const bool fused = phases == (VM_PHASE_ROUTER | VM_PHASE_EXPERTS);
   hipError_t e = hipSuccess;
+  vm::FusedLaunch fl{};
+  uint32_t blocks = 0;
+  bool two_launch = false;
+  if (fused && fused_args(a, w, ws, fl, blocks, two_launch)) {
+    e = vm::launch_fused_front(fl, stream);
+    if (e != hipSuccess) return hip_fail(e, "router launch");
+    e = vm::launch_fused_experts(fl, blocks, two_launch, stream);
+    if (e != hipSuccess) return hip_fail(e, "experts launch");
+    if (two_launch) return VM_OK;
+    e = vm::launch_down(down_args(a, w, ws, words, nullptr, scores), stream);
+    if (e != hipSuccess) return hip_fail(e, "down launch");
+    return VM_OK;
+  }
 
   if (phases & VM_PHASE_ROUTER) {
     e = launch_layer_front(a, w, ws, stream);
@@ -581,28 +699,9 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
   e = vm::launch_gateup(g, stream);
   if (e != hipSuccess) return hip_fail(e, "gate/up launch");
 
-  vm::DownLaunch d{};
-  d.act = ws + w.act;
-  d.routes = fused ? words : reinterpret_cast<const uint32_t*>(inds);
-  d.slot_table = fused ? nullptr : a->slot_table;
-  d.down = to_ptrs(a->down);
-  if (shared) d.shared_down = to_ptrs(a->shared_down_proj);
-  d.shared_sig = ws + w.sig;
-  d.pool = to_pool(a->pool);
-  d.scores = scores;
-  d.score_dtype = static_cast<int>(a->act_dtype);
-  d.out = a->output;
-  d.inject = to_inject(a);
-  d.generic = a->combine == VM_COMBINE_GENERIC ? 1u : 0u;
-  d.status = a->status;
-  d.tokens = T;
-  d.slots = K;
-  d.hidden = H;
-  d.inter = I;
-  d.experts = E;
-  d.has_shared = shared ? 1 : 0;
-  d.act_dtype = static_cast<int>(a->act_dtype);
-  e = vm::launch_down(d, stream);
+  e = fused ? vm::launch_down(down_args(a, w, ws, words, nullptr, scores), stream)
+            : vm::launch_down(down_args(a, w, ws, reinterpret_cast<const uint32_t*>(inds), a->slot_table, scores),
+                              stream);
   if (e != hipSuccess) return hip_fail(e, "down launch");
   return VM_OK;
 }
@@ -736,8 +835,13 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
     return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)w.total);
   char* ws = static_cast<char*>(a->workspace);
 
-  // 1. router logits and shared gate
-  hipError_t e = launch_layer_front(a, w, ws, stream);
+  // 1. router logits and shared gate (with the one-token pipeline: also the
+  //    shared expert's gate/up)
+  vm::FusedLaunch fl{};
+  uint32_t blocks = 0;
+  bool two_launch = false;
+  const bool one_token = fused_args(&r, w, ws, fl, blocks, two_launch);
+  hipError_t e = one_token ? vm::launch_fused_front(fl, stream) : launch_layer_front(a, w, ws, stream);
   if (e != hipSuccess) return hip_fail(e, "router launch");
   // 2. softmax/top-k into inds/scores and assign() on the device state, one block
   int32_t* inds = a->inds_out != nullptr ? a->inds_out : reinterpret_cast<int32_t*>(ws + w.inds);
@@ -785,6 +889,18 @@ int vm_moe_layer_lru(const VmLayerArgs* a, const VmDeviceLru* lru, void* stream_
   e = vm::launch_fill(f, stream);
   if (e != hipSuccess) return hip_fail(e, "fill launch");
   // 4. the experts through the updated slot table
+  if (one_token) {
+    fl.routes = inds;
+    fl.route_scores = static_cast<const uint16_t*>(sel.scores);
+    fl.inds_out = nullptr;
+    fl.scores_out = nullptr;
+    e = vm::launch_fused_experts(fl, blocks, two_launch, stream);
+    if (e != hipSuccess) return hip_fail(e, "experts launch");
+    if (two_launch) return VM_OK;
+    e = vm::launch_down(down_args(&r, w, ws, fl.words_out, nullptr, sel.scores), stream);
+    if (e != hipSuccess) return hip_fail(e, "down launch");
+    return VM_OK;
+  }
   r.phases = VM_PHASE_EXPERTS;
   return layer_decode(&r, stream);
 }
@@ -1084,6 +1200,12 @@ int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride,
 }
 
 // ------------------------------------------------------------- timing ---
+
+int vm_decode_pipeline(int mode) {
+  if (mode < -1 || mode > 2) return fail(VM_EINVAL, "mode must be -1 (query) or 0..2");
+  if (mode == -1) return g_fused_decode.load();
+  return g_fused_decode.exchange(mode);
+}
 
 int vm_timing_enable(int enabled) {
   Timing& t = timing();

@@ -96,6 +96,63 @@ struct DownLaunch {
   uint32_t generic;            // 1: generic combine (products rounded before the slot sum)
 };
 
+// ---------------------------------------------------- fused decode (T = 1) --
+// A decode call of one token (fused.hip): the front (router logits, the
+// shared expert's gate/up + SwiGLU and its sigmoid gate) and one grid of a
+// block per CU for the routed experts: either gate/up only, followed by the
+// down kernel, or gate/up and every slot's down rows with the activations
+// handed over through tagged words (two launches).
+constexpr int kFusedMaxGateUp = 4;     // gate/up items per wave of the experts grid
+constexpr int kFusedMaxDown = 4;       // down items per wave
+constexpr uint32_t kFusedMaxSlots = 11;    // top_k (<= 10) + the shared expert
+constexpr uint32_t kFusedMaxInter = 2048;
+// Hand-off word w lives at tag_index(w): every 128-byte line of 32 words on a
+// 4 KiB page of its own, so the reads of every block spread over the memory
+// channels instead of queueing on the few that one dense array maps to.
+constexpr uint32_t kTagLineWords = 32;
+constexpr uint32_t kTagLineStride = 1024;
+__host__ __device__ inline size_t tag_index(uint32_t w) {
+  return static_cast<size_t>(w / kTagLineWords) * kTagLineStride + (w % kTagLineWords);
+}
+__host__ __device__ inline size_t tag_words(uint32_t count) {
+  return static_cast<size_t>((count + kTagLineWords - 1) / kTagLineWords) * kTagLineStride;
+}
+
+struct FusedLaunch {
+  const uint16_t* x;           // [H] bf16
+  const uint16_t* router;      // [E, H] bf16
+  const float* router_bias;    // optional [E]
+  float* logits;               // [E], rounded to bf16
+  ProjPtrs sh_gate, sh_up, sh_down, sh_seg;  // shared expert and its H -> 1 gate (has_shared)
+  uint16_t* sh_act;            // [I] SwiGLU of the shared expert
+  uint16_t* sh_sig;            // [1] sigmoid of the shared gate
+  const int32_t* routes;       // [K] expert ids chosen elsewhere (device LRU); null: select from logits
+  const uint16_t* route_scores;  // [K] their bf16 scores
+  const int32_t* slot_table;   // expert -> pool slot, or null for dense banks
+  PoolDev pool;
+  ProjPtrs gate, up, down;     // dense routed banks
+  uint32_t* act_tag;           // two launches: [K, I] hand-off words (1 << 16 | bf16), zeroed by the front
+  uint16_t* act;               // three launches: [K + 1, I] activations (the shared expert's at K)
+  uint32_t* words_out;         // three launches: [K] route words for the down kernel
+  uint16_t* out;               // [H]
+  int32_t* inds_out;           // optional [K]
+  uint16_t* scores_out;        // optional [K]
+  uint32_t* status;            // bit 0: unresolved expert, bit 5: hand-off wait gave up
+  uint64_t* trace;
+  Inject inject;
+  uint32_t hidden, inter, experts, slots, has_shared, generic;
+  float blend;
+  uint32_t gu_items, dn_tiles;  // gate/up row groups and down row tiles of the experts grid
+};
+
+// Launch shape of the fused decode for a layer shape, or false when the
+// three-launch path must run it (grid = blocks of the experts kernel).
+bool fused_plan(uint32_t hidden, uint32_t inter, uint32_t slots, uint32_t has_shared, uint32_t experts,
+                uint32_t blocks, FusedLaunch& p);
+hipError_t launch_fused_front(const FusedLaunch& p, hipStream_t stream);
+// down: the two-launch experts grid; otherwise its gate/up part only
+hipError_t launch_fused_experts(const FusedLaunch& p, uint32_t blocks, bool down, hipStream_t stream);
+
 // ------------------------------------------------------ device-side LRU --
 constexpr uint32_t kLruMaxRouted = 80;  // VM_LAYER_MAX_TOKENS * MAX_TOP_K
 constexpr int kLruThreads = 1024;       // one block runs the selection and the assign
