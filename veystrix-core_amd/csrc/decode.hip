@@ -208,9 +208,14 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
 
   // 1. loads: the selection's logits and slot-table entries first, then this
   //    lane's activation groups
+  // wave 0 selects for the block (the same pair for every wave) and hands the
+  // route word over through LDS: the selection is VALU-bound, so doing it in
+  // every wave only crowded the SIMDs
+  __shared__ uint32_t s_word;
+  const bool chooser = select && wave == 0;
   float lg[kMaxExpertsPerLane];
   int32_t tab[kMaxExpertsPerLane];
-  if (select) {
+  if (chooser) {
     load_logits(p.logits + static_cast<size_t>(t) * E, E, lane, lg);
     if (p.slot_table != nullptr) {
 #pragma unroll
@@ -230,19 +235,24 @@ __global__ __launch_bounds__(kGuBlock) void k_gateup(GateUpLaunch p) {
   GateKeys<A> keys;
   uint32_t word = 0;
   if (select) {
-    softmax_keys<A>(lg, E, lane, keys);
-    if (p.trace != nullptr) tr.mark(5);
-    const uint32_t e = select_rank<A>(keys, p.slots, j, lane, s_cand);
-    word = e;
-    if (p.slot_table != nullptr) {
-      const uint32_t m_e = e >> 6, l_e = e & 63u;
-      int32_t slot = -1;
+    if (chooser) {
+      softmax_keys<A>(lg, E, lane, keys);
+      if (p.trace != nullptr) tr.mark(5);
+      const uint32_t e = select_rank<A>(keys, p.slots, j, lane, s_cand);
+      word = e;
+      if (p.slot_table != nullptr) {
+        const uint32_t m_e = e >> 6, l_e = e & 63u;
+        int32_t slot = -1;
 #pragma unroll
-      for (int m = 0; m < kMaxExpertsPerLane; ++m)
-        if (m == static_cast<int>(m_e)) slot = __builtin_amdgcn_readlane(tab[m], l_e);
-      word = route_word(slot);
+        for (int m = 0; m < kMaxExpertsPerLane; ++m)
+          if (m == static_cast<int>(m_e)) slot = __builtin_amdgcn_readlane(tab[m], l_e);
+        word = route_word(slot);
+      }
+      if (lane == 0) s_word = word;
+      if (p.trace != nullptr) tr.mark(6);
     }
-    if (p.trace != nullptr) tr.mark(6);
+    lds_barrier();
+    word = s_word;
   } else if (!shared_pair) {
     word = p.routes[t * p.slots + j];
   }
