@@ -358,6 +358,22 @@ int vm_moe_layer(const VmLayerArgs* args, void* stream);
 /* Workspace: vm_moe_layer_workspace() of the same shape. */
 int vm_moe_layer_lru(const VmLayerArgs* args, const VmDeviceLru* lru, void* stream);
 
+/* vm_moe_layer_static: vm_moe_layer with the library's own scratch in place
+ * of args->workspace / workspace_bytes (both ignored).  It allocates nothing
+ * (no hipMalloc, hipFree or allocating library call), for callers that cannot
+ * allocate: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  No counterpart in the reference.  The scratch is a static
+ * device array of VM_STATIC_SCRATCH_BYTES on each GPU the library runs on,
+ * held until the process ends; a call whose vm_moe_layer_workspace() exceeds
+ * it fails with VM_EWORKSPACE.  Every call on one GPU shares that GPU's
+ * array and leaves its contents behind: calls that overlap on one GPU (two
+ * streams, two threads) race.  A router-only call followed by an
+ * experts-only call (VM_PHASE_*) works as with one workspace, provided no
+ * other call on that GPU runs in between.  The stream must belong to the
+ * current device. */
+#define VM_STATIC_SCRATCH_BYTES (4ull << 20)
+int vm_moe_layer_static(const VmLayerArgs* args, void* stream);
+
 /* The hyper-connection before a branch (see VmHyperArgs): two launches. */
 uint64_t vm_hyper_mix_workspace(uint32_t tokens, uint32_t hc_count, uint32_t hidden_size, uint32_t lowrank,
                                 uint32_t act_dtype);

@@ -205,3 +205,24 @@ def test_layer_injection_is_validated_without_a_device():
     a.inject_hidden, a.inject_weights, a.hc_count = 16384, 20480, 9
     assert _lib.lib().vm_moe_layer(ctypes.byref(a), None) == _lib.VM_EINVAL
     assert "hc_count" in _lib.last_error()
+
+
+def test_static_layer_refuses_calls_above_its_scratch_without_a_device():
+    text = open(HEADER).read()
+    assert re.search(r"#define VM_STATIC_SCRATCH_BYTES \(4ull << 20\)", text)
+    assert _lib.VM_STATIC_SCRATCH_BYTES == 4 << 20
+    lib = _lib.lib()
+    a = _lib.VmLayerArgs()
+    a.x, a.output, a.router_weight = 256, 512, 768
+    a.tokens, a.hidden_size, a.inter_size, a.expert_count, a.top_k, a.group_size = 2048, 2048, 512, 512, 10, 32
+    a.gate.weight = a.up.weight = a.down.weight = 4096
+    a.gate.scales = a.up.scales = a.down.scales = 8192
+    a.gate.biases = a.up.biases = a.down.biases = 8192
+    need = lib.vm_moe_layer_workspace(2048, 10, 2048, 512, 0, 512, 0)
+    assert need > _lib.VM_STATIC_SCRATCH_BYTES
+    assert lib.vm_moe_layer_static(ctypes.byref(a), None) == _lib.VM_EWORKSPACE
+    assert "static" in _lib.last_error() and str(need) in _lib.last_error()
+    a.tokens = 8   # a decode call fits; the argument checks still come first
+    assert lib.vm_moe_layer_workspace(8, 10, 2048, 512, 0, 512, 0) <= _lib.VM_STATIC_SCRATCH_BYTES
+    a.router_weight = 770
+    assert lib.vm_moe_layer_static(ctypes.byref(a), None) == _lib.VM_EINVAL

@@ -152,6 +152,39 @@ bool timing_events(const char* family, hipEvent_t* start, hipEvent_t* stop) {
 
 }  // namespace vm
 
+// The workspace of vm_moe_layer_static: one array per device in the library's
+// own device memory, held until the process ends.  On the host, `scratch`
+// names a stand-in, not a device address: host code uses only the address
+// that hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) unsigned char scratch[VM_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices];
+
+// This device's scratch address, looked up once per device with the device
+// current.
+int scratch_address(void** out) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(VM_EUNSUPPORTED, "device %d is beyond the scratch table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t s = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (s != hipSuccess) return hip_fail(s, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(VM_EHIP, "hipGetSymbolAddress(scratch) returned no address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return VM_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int vm_abi_version(void) { return VM_ABI_VERSION; }
@@ -572,6 +605,23 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
     if (rc != VM_OK) return rc;
   }
   return VM_OK;
+}
+
+int vm_moe_layer_static(const VmLayerArgs* a, void* stream_ptr) {
+  int rc = validate_layer(a);
+  if (rc != VM_OK) return rc;
+  const uint64_t need = vm_moe_layer_workspace(a->tokens, a->top_k, a->hidden_size, a->inter_size, a->shared_inter,
+                                               a->expert_count, a->act_dtype);
+  if (need > VM_STATIC_SCRATCH_BYTES)
+    return fail(VM_EWORKSPACE, "this call needs %llu bytes of scratch, above the static %llu; call vm_moe_layer "
+                "with a workspace", (unsigned long long)need, (unsigned long long)VM_STATIC_SCRATCH_BYTES);
+  void* ptr = nullptr;
+  rc = scratch_address(&ptr);
+  if (rc != VM_OK) return rc;
+  VmLayerArgs c = *a;
+  c.workspace = ptr;
+  c.workspace_bytes = VM_STATIC_SCRATCH_BYTES;
+  return vm_moe_layer(&c, stream_ptr);
 }
 
 // Router logits (and the shared expert's sigmoid gate) of a decode call.

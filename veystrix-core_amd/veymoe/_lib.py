@@ -18,6 +18,7 @@ VM_EINVAL = -1
 VM_EUNSUPPORTED = -2
 VM_EHIP = -3
 VM_EWORKSPACE = -4
+VM_STATIC_SCRATCH_BYTES = 4 << 20  # vm_moe_layer_static's per-device scratch
 VM_BF16 = 0
 VM_F32 = 1
 VM_SLOT_BIT = 0x80000000
@@ -186,6 +187,7 @@ SIGNATURES = {
     "vm_moe_layer_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_moe_layer": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), _vp]),
     "vm_moe_layer_lru": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), ctypes.POINTER(VmDeviceLru), _vp]),
+    "vm_moe_layer_static": (ctypes.c_int, [ctypes.POINTER(VmLayerArgs), _vp]),
     "vm_hyper_mix_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
     "vm_hyper_mix": (ctypes.c_int, [ctypes.POINTER(VmHyperArgs), _vp]),
     "vm_moe_grouped_workspace": (_c_u64, [_c_u32, _c_u32, _c_u32, _c_u32, _c_u32, _c_u32]),
