@@ -153,17 +153,57 @@ def test_grouped_prefill_matches_decode_rows(device):
     _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, "prefill sample vs oracle")
 
 
+def test_grouped_router_against_the_decode_router_over_8192_rows(device):
+    """The rate at which the grouped (MFMA) router and the decode (v_dot2)
+    router pick different expert sets for the same token, over 8192 tokens
+    at the full prefill shape: the layer in 2048-row calls (MFMA router)
+    against vm_router_topk, which sums every logit in the decode order at
+    any row count.  Calls of up to 64 rows route with the decode router, so
+    only calls above that can differ; the differing rows must be near ties
+    and their count is printed."""
+    from veymoe.router import router_topk
+
+    spec = synth.CONFIGS["prefill"]
+    seed = 331
+    pool = ExpertPool(spec.layout, spec.experts, layers=1, experts=spec.experts, device=device)
+    layer = assemble.build_layer(spec, seed, device, pool=pool)
+    rows = 8192
+    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, rows))
+    x = bf16_device(x_np, device)
+    grouped = []
+    for c in range(0, rows, 2048):
+        layer(x[c:c + 2048].contiguous())
+        grouped.append(layer.last_inds.clone())
+    grouped = torch.cat(grouped).sort(dim=1).values
+    bias = layer.gate.bias.float() if layer.gate.bias is not None else None
+    decode, _ = router_topk(x, layer.gate.weight, spec.top_k, logit_bias=bias)
+    decode = decode.sort(dim=1).values
+    torch.cuda.synchronize()
+    differ = np.nonzero(~(grouped == decode).all(dim=1).cpu().numpy())[0]
+    print(f"[selection] grouped vs decode router over {rows} rows: {len(differ)} rows differ "
+          f"({len(differ) / rows:.2e})", flush=True)
+    if len(differ):
+        layer_np = synth.numpy_layer(spec, seed)
+        _, _, gates = mo.route(x_np[differ], layer_np["router"], spec.top_k, "bf16", layer_np["router_bias"])
+        for i in range(len(differ)):
+            assert _near_tie(gates[i], spec.top_k), int(differ[i])
+    assert len(differ) <= rows // 1000
+
+
 def _switch(np_packs, hidden, inter, experts, device):
     return HipSwitchGLU(hidden, inter, experts, projections=to_device(np_packs, device))
 
 
 @pytest.mark.parametrize("mode", [COMBINE_NONE, COMBINE_GENERIC, COMBINE_FUSED])
-def test_grouped_experts_modes(device, mode):
-    hidden, inter, experts, tokens, k = 256, 128, 12, 150, 3
+@pytest.mark.parametrize("tokens,crowd", [(150, 100), (60, 40)], ids=["64-row-tiles", "16-row-tiles"])
+def test_grouped_experts_modes(device, mode, tokens, crowd):
+    """150 tokens run the 64-row tile GEMM, 60 the 16-row tile kernels; one
+    expert takes `crowd` rows, so it spans two (three) tiles."""
+    hidden, inter, experts, k = 256, 128, 12, 3
     np_packs = packs(41, hidden, inter, experts)
     rng = np.random.default_rng(42)
     inds = np.stack([rng.choice(experts, k, replace=False) for _ in range(tokens)]).astype(np.int32)
-    inds[:100, 0] = 5                       # expert 5: > 64 rows, two row tiles
+    inds[:crowd, 0] = 5                     # expert 5: several row tiles
     scores = mo.bf16r(rng.uniform(0.05, 0.6, (tokens, k)).astype(np.float32))
     x_np = mo.bf16r(rng.normal(size=(tokens, hidden)).astype(np.float32))
     shared_y = mo.bf16r(rng.normal(0, 0.1, (tokens, hidden)).astype(np.float32))

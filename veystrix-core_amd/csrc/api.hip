@@ -484,15 +484,31 @@ static bool fused_args(const VmLayerArgs* a, const LayerWs& w, char* ws, vm::Fus
 struct GroupedWs {
   uint64_t logits, sig, inds, scores, row_off, tiles, tile_count, tiles_dn, tile_count_dn, sort_counts,
       sort_cursors, row_token, pair_row, act, rows, total;
-  uint32_t rows_total, groups, max_tiles, max_tiles_dn;
+  uint32_t rows_total, groups, max_tiles, max_tiles_dn, tile_rows, tile_rows_dn;
+  bool small;  // 16-row tile kernels (k_rows)
 };
+
+// Calls of up to this many tokens run the 16-row tile kernels, whose blocks
+// stage their tile's A rows once and stream the weights without barriers:
+// with few rows per expert the chunked GEMM's 64-row tiles ran mostly empty.
+constexpr uint32_t kRowsMaxTokens = 64;
+
+#ifndef VM_ROWS_PATH
+#define VM_ROWS_PATH 1
+#endif
+static bool small_grouped(uint32_t T, uint32_t H, uint32_t I) {
+  return VM_ROWS_PATH && T <= kRowsMaxTokens && vm::rows_supported(H) && vm::rows_supported(I);
+}
 
 static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint32_t E, bool shared) {
   GroupedWs w{};
   w.rows_total = T * K + (shared ? T : 0);
   w.groups = E + (shared ? 1 : 0);
-  w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups, vm::kGroupedRows);
-  w.max_tiles_dn = vm::grouped_max_tiles(w.rows_total, w.groups, vm::kGroupedRowsDown);
+  w.small = small_grouped(T, H, I);
+  w.tile_rows = w.small ? vm::kRowsTile : vm::kGroupedRows;
+  w.tile_rows_dn = w.small ? vm::kRowsTile : vm::kGroupedRowsDown;
+  w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows);
+  w.max_tiles_dn = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows_dn);
   uint64_t o = kAlign;
   auto take = [&](uint64_t bytes) {
     const uint64_t at = o;
@@ -994,6 +1010,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   s.slots = g.K;
   s.experts = g.E;
   s.shared_rows = g.shared ? g.T : 0;
+  s.tile_rows = w.tile_rows;
+  s.tile_rows_dn = w.tile_rows_dn;
   hipError_t e = vm::launch_sort(s, stream);
   if (e != hipSuccess) return hip_fail(e, "sort launch");
 
@@ -1020,7 +1038,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.k_dim = g.H;
   q.n_dim = g.I;
   q.a_stride = g.H;
-  e = vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
+  e = w.small ? vm::launch_rows(vm::kEpiSwiglu, q, w.max_tiles, stream)
+              : vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped gate/up launch");
   // down over the contiguous activation rows
   q.a = reinterpret_cast<const uint16_t*>(ws + w.act);
@@ -1036,7 +1055,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.a_stride = g.I;
   q.tiles = s.tiles_dn;
   q.tile_count = s.tile_count_dn;
-  e = vm::launch_grouped(vm::kEpiRows, q, w.max_tiles_dn, stream);
+  e = w.small ? vm::launch_rows(vm::kEpiRows, q, w.max_tiles_dn, stream)
+              : vm::launch_grouped(vm::kEpiRows, q, w.max_tiles_dn, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped down launch");
 
   vm::CombineLaunch c{};

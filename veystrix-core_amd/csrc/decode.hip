@@ -40,7 +40,11 @@ namespace vm {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / 64;
+// router front: waves per block (one router row per wave)
+#ifndef VM_FRONT_WAVES
+#define VM_FRONT_WAVES 4
+#endif
+constexpr int kFrontW = VM_FRONT_WAVES;
 // block shapes of the full-width (hidden >= 2048) decode GEMVs: output rows per
 // lane group in gate/up, row groups per block in down
 #ifndef VM_GATEUP_ROWS
@@ -126,7 +130,7 @@ __global__ __launch_bounds__(kLruThreads) void k_select_lru(SelectLaunch p, LruL
 // tokens of grid row y; the blocks after them: the shared gate, one wave per
 // token of that row.
 template <class A, int CH>
-__global__ __launch_bounds__(kBlock) void k_front(FrontLaunch p, uint32_t router_blocks) {
+__global__ __launch_bounds__(kFrontW * 64) void k_front(FrontLaunch p, uint32_t router_blocks) {
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = threadIdx.x >> 6;
   PhaseTrace tr;
@@ -134,10 +138,10 @@ __global__ __launch_bounds__(kBlock) void k_front(FrontLaunch p, uint32_t router
   const uint32_t t_begin = blockIdx.y * kFrontTokens;
   const uint32_t t_end = min(p.tokens, t_begin + kFrontTokens);
   if (blockIdx.x >= router_blocks) {
-    const uint32_t t = t_begin + (blockIdx.x - router_blocks) * kWaves + wave;
+    const uint32_t t = t_begin + (blockIdx.x - router_blocks) * kFrontW + wave;
     if (t < t_end) shared_gate_token<A>(p, t, lane);
   } else {
-    const uint32_t row = blockIdx.x * kWaves + wave;
+    const uint32_t row = blockIdx.x * kFrontW + wave;
     if (row < p.experts) {
       if (t_end - t_begin == 1) router_row<A, CH, 1>(p, row, lane, t_begin, t_end);
       else router_row<A, CH, kFrontUnroll>(p, row, lane, t_begin, t_end);
@@ -642,10 +646,10 @@ hipError_t down_dispatch(const DownLaunch& p, hipStream_t stream) {
 
 template <class A>
 hipError_t front_go(const FrontLaunch& p0, hipStream_t stream) {
-  const uint32_t router_blocks = (p0.experts + kWaves - 1) / kWaves;
+  const uint32_t router_blocks = (p0.experts + kFrontW - 1) / kFrontW;
   const uint32_t row_tokens = p0.tokens < kFrontTokens ? p0.tokens : kFrontTokens;
-  const uint32_t shared_blocks = p0.seg.w != nullptr ? (row_tokens + kWaves - 1) / kWaves : 0;
-  const dim3 grid(router_blocks + shared_blocks, (p0.tokens + kFrontTokens - 1) / kFrontTokens), block(kBlock);
+  const uint32_t shared_blocks = p0.seg.w != nullptr ? (row_tokens + kFrontW - 1) / kFrontW : 0;
+  const dim3 grid(router_blocks + shared_blocks, (p0.tokens + kFrontTokens - 1) / kFrontTokens), block(kFrontW * 64);
   FrontLaunch p = p0;
   p.trace = trace_reserve(grid.x * grid.y);
   const uint32_t chunks = (p.hidden / 8 + 63) / 64;

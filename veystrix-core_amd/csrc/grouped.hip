@@ -43,6 +43,7 @@ namespace vm {
 namespace {
 
 constexpr int kGB = 256;                 // threads per block of the small kernels
+constexpr int kCombineSlots = 10;        // top-k bound of the combine (the layer's MAX_TOP_K)
 #ifndef VM_GCG
 #define VM_GCG 8
 #endif
@@ -618,6 +619,246 @@ void k_grouped(GroupedLaunch p) {
   grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1>(p, w, row0, rows, slice, s_a0);
 }
 
+// ------------------------------------------------------------- row tiles ---
+
+// Small calls: every tile holds at most 16 rows of one group (one MFMA row
+// block), so the chunked GEMM's per-chunk A staging and barriers would only
+// serialise the weight stream.  Here the block stages its tile's A rows over
+// the whole K in LDS once and each wave streams its own 16 weight columns of
+// every projection straight into its MFMA lanes, kRowsDepth chunks ahead,
+// with no barrier in the K loop.
+//
+// K order: lane quarter q = lane / 16 owns the contiguous quarter of the
+// groups [q G/4, (q + 1) G/4); MFMA step j feeds packed word j % 4 of the
+// quarter's group j / 4.  So a lane's scales and biases for the whole K are
+// 2 KCH contiguous bf16 values (loaded once per tile with wide loads: 2-byte
+// loads per lane and chunk had cost more than the weights), and its weights
+// of a chunk (two groups) are 32 contiguous bytes.  The fp32 sums over K run
+// in a different order from the chunked GEMM, within the same tolerance.
+// A row r stores its 16-byte unit u at (u & ~15) | ((u ^ rows_swz(r, q)) & 15):
+// at step j the 64 lanes (16 rows x 4 quarters) read units q G/4*4 + j, which
+// this spreads over all 16 bank groups, four lanes each.
+constexpr int kRowsDepth = 3;  // chunks of weight loads in flight per wave
+
+__device__ __forceinline__ constexpr uint32_t rows_swz(uint32_t r, uint32_t q) { return (r ^ (q << 2)) & 15u; }
+
+// n consecutive dwords from a 4-byte aligned address, in the widest loads
+template <int N>
+__device__ __forceinline__ void ldg_dwords(const uint8_t* src, uint32_t (&out)[N]) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const uint4 v = ldg16(src + 4 * i);
+      out[i] = v.x; out[i + 1] = v.y; out[i + 2] = v.z; out[i + 3] = v.w;
+    }
+  } else if constexpr (N == 2) {
+    const uint2 v = *reinterpret_cast<const uint2*>(src);
+    out[0] = v.x; out[1] = v.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = *reinterpret_cast<const uint32_t*>(src + 4 * i);
+  }
+}
+
+// One (tile, column slice) item of block-uniform index `item`; false when the
+// item is past the live tiles.  KCH: K = 256 KCH (the instance is picked per
+// K), so the kernel is straight-line and every wait counts exactly the loads
+// it needs.  Load order: the tile's row indices (lanes 0-15), its A rows, the
+// lane's scales and biases, the first kRowsDepth chunks of weights; the A
+// rows go to LDS as they arrive, with the weight loads still in flight.
+template <int EPI, int WAVES, int PROJ, int KCH>
+__device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item, uint8_t* s_a, PhaseTrace& tr) {
+  constexpr int kThreads = WAVES * 64;
+  constexpr int kCols = WAVES * 16;
+  constexpr int kG = KCH * 8;                      // groups of K
+  constexpr int kQG = kG / 4;                      // groups per lane quarter (2 KCH)
+  constexpr int kUnits = kG * 4;                   // 16-byte A units per row
+  constexpr int kRowBytes = kUnits * 16;
+  constexpr int kItems = 16 * kUnits / kThreads;   // A units per thread
+  static_assert((16 * kUnits) % kThreads == 0, "whole A units per thread");
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t K = p.k_dim, N = p.n_dim;
+
+  // XCD-aware order: the column slices of a tile take consecutive blocks of
+  // one XCD (block L runs on XCD L % 8) and share its L2 copy of the A rows
+  const uint32_t slices = (N + kCols - 1) / kCols;
+  const uint32_t r8 = item >> 3;
+  const uint32_t slice = r8 % slices;
+  const uint32_t tile = (r8 / slices) * 8 + (item & 7u);
+  if (tile >= *p.tile_count) return false;
+  const uint2 td = p.tiles[tile];
+  const uint32_t group = td.x;
+  const uint32_t row0 = p.row_off[group] + td.y;
+  const uint32_t rows = min(p.row_off[group + 1] - row0, 16u);
+
+  // the A row of each of the tile's rows, held by lanes 0-15 of every wave
+  uint32_t my_row = row0;
+  if (lane < rows) my_row = p.row_token != nullptr ? p.row_token[row0 + lane] : row0 + lane;
+
+  ProjPtrs w[PROJ];
+  bool ok = true;
+  if (group >= p.experts) {
+#pragma unroll
+    for (int pj = 0; pj < PROJ; ++pj) w[pj] = p.shared[pj];
+    ok = w[0].w != nullptr;
+  } else {
+    uint32_t index = 0;
+    const int kind = resolve_word(group, p.slot_table, p.experts, p.pool, &p.stream, p.dense[0].w != nullptr, index);
+    ok = kind != kSrcNone;
+#pragma unroll
+    for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
+  }
+  if (!ok) {  // an unresolved expert: its rows are zero (status flagged)
+    if (tid == 0 && slice == 0) flag(p.status, 1u);
+    for (uint32_t i = tid; i < rows * kCols; i += kThreads) {
+      const uint32_t col = slice * kCols + i % kCols;
+      if (col < N) ActBF16::store(p.out, static_cast<size_t>(row0 + i / kCols) * N + col, 0.0f);
+    }
+    return true;
+  }
+  if (p.trace != nullptr) tr.mark(1);
+
+  // A loads: unit it = j * threads + tid -> (row it / kUnits, unit it % kUnits).
+  // Unconditional (branches here made every load wait for the one before):
+  // rows past the tile reload its last row (their outputs are not stored; an
+  // MFMA output row depends on its own A row only).
+  const bool gather = p.row_token != nullptr;
+  uint4 av[kItems];
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const uint32_t it = j * kThreads + tid;
+    const uint32_t r = min(it / kUnits, rows - 1), u = it % kUnits;
+    uint32_t arow;
+    if constexpr (kUnits % 64 == 0) {  // r is wave-uniform
+      arow = gather ? __builtin_amdgcn_readlane(my_row, __builtin_amdgcn_readfirstlane(r)) : row0 + r;
+    } else {
+      arow = gather ? __shfl(my_row, static_cast<int>(r), 64) : row0 + r;
+    }
+    av[j] = ldg16(p.a + static_cast<size_t>(arow) * p.a_stride + u * 8u);
+  }
+
+  // B: lane -> column lane % 16 of the wave's block, quarter q = lane / 16;
+  // columns past N read the last row and are not stored
+  const uint32_t bn = lane & 15u, q = lane >> 4;
+  const uint32_t n_col = slice * kCols + wave * 16 + bn;
+  const uint32_t col_ld = min(n_col, N - 1);
+  const uint32_t g_lane = q * kQG;                 // the lane's first group
+  uint32_t sv[PROJ][KCH], bv[PROJ][KCH];           // bf16 pairs of groups g_lane + 2 i, + 2 i + 1
+#pragma unroll
+  for (int pj = 0; pj < PROJ; ++pj) {
+    const size_t m = (static_cast<size_t>(col_ld) * kG + g_lane) * 2u;
+    ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].s) + m, sv[pj]);
+    ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].b) + m, bv[pj]);
+  }
+  const uint8_t* wl[PROJ];
+#pragma unroll
+  for (int pj = 0; pj < PROJ; ++pj)
+    wl[pj] = reinterpret_cast<const uint8_t*>(w[pj].w) + (static_cast<size_t>(col_ld) * kG + g_lane) * 16u;
+  constexpr int kDepth = KCH < kRowsDepth ? KCH : kRowsDepth;
+  uint4 bw[kDepth][PROJ][2];
+  // keep the prefetch here and in chunk order: the scheduler otherwise sinks
+  // every chunk's loads to just before their first use, or mixes the chunks,
+  // and each chunk then waits for all outstanding loads
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int d = 0; d < kDepth; ++d) {
+#pragma unroll
+    for (int pj = 0; pj < PROJ; ++pj) {
+      bw[d][pj][0] = ldg16(wl[pj] + d * 32u);
+      bw[d][pj][1] = ldg16(wl[pj] + d * 32u + 16u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  if (p.trace != nullptr) tr.mark(2);
+#pragma unroll
+  for (int j = 0; j < kItems; ++j) {
+    const uint32_t it = j * kThreads + tid;
+    const uint32_t r = it / kUnits, u = it % kUnits;
+    const uint4 x = av[j];
+    const uint4 pp = make_uint4((x.x & 0xffffu) | (x.z << 16), (x.x >> 16) | (x.z & 0xffff0000u),
+                                (x.y & 0xffffu) | (x.w << 16), (x.y >> 16) | (x.w & 0xffff0000u));
+    const uint32_t phys = (u & ~15u) | ((u ^ rows_swz(r, u / (kQG * 4))) & 15u);
+    *reinterpret_cast<uint4*>(s_a + r * kRowBytes + phys * 16u) = pp;
+  }
+  __syncthreads();
+  if (p.trace != nullptr) tr.mark(3);
+
+  f32x4_t acc[PROJ];
+#pragma unroll
+  for (int pj = 0; pj < PROJ; ++pj) acc[pj] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t magic = f16_magic();
+  const uint32_t am = lane & 15u;
+  const uint8_t* a_lane = s_a + am * kRowBytes;
+  const uint32_t a_sw = rows_swz(am, q);
+  const uint32_t u_lane = q * kQG * 4;             // the lane's first A unit
+#pragma unroll
+  for (int c = 0; c < KCH; ++c) {
+    const int d = c % kDepth;
+#pragma unroll
+    for (int st = 0; st < 8; ++st) {
+      const int gi = 2 * c + (st >> 2);            // group of the lane's quarter
+      const uint32_t u = u_lane + gi * 4 + (st & 3);
+      const uint32_t phys = (u & ~15u) | ((u ^ a_sw) & 15u);
+      const bf16x8_t aop = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const uint4*>(a_lane + phys * 16u));
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) {
+        const uint32_t s2 = sv[pj][gi >> 1], b2 = bv[pj][gi >> 1];
+        const Dequant dq(__uint_as_float((gi & 1) ? s2 & 0xffff0000u : s2 << 16),
+                         __uint_as_float((gi & 1) ? b2 & 0xffff0000u : b2 << 16));
+        const uint4 wv = bw[d][pj][st >> 2];
+        const int i = st & 3;
+        uint32_t r4[4];
+        dq.word(i == 0 ? wv.x : i == 1 ? wv.y : i == 2 ? wv.z : wv.w, magic, r4);
+        acc[pj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop, as_operand(r4), acc[pj], 0, 0, 0);
+      }
+    }
+    if (c + kDepth < KCH) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) {
+        bw[d][pj][0] = ldg16(wl[pj] + (c + kDepth) * 32u);
+        bw[d][pj][1] = ldg16(wl[pj] + (c + kDepth) * 32u + 16u);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  if (p.trace != nullptr) tr.mark(4);
+  // epilogue: lane holds rows 4 (lane / 16) + i, column lane % 16
+  if (n_col >= N) return true;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t r = 4 * q + i;
+    if (r >= rows) continue;
+    const size_t o = static_cast<size_t>(row0 + r) * N + n_col;
+    if constexpr (EPI == kEpiSwiglu) {
+      ActBF16::store(p.out, o, swiglu_act<ActBF16>(round_bf16(acc[0][i]), round_bf16(acc[PROJ - 1][i])));
+    } else {
+      ActBF16::store(p.out, o, round_bf16(acc[0][i]));
+    }
+  }
+  return true;
+}
+
+// One item per block over the bound of the live tiles (blocks past them exit).
+// A loop of items per block kept loop-invariant arguments live and took the
+// registers of a second block per CU.
+template <int EPI, int WAVES, int PROJ, int KCH>
+__global__ __launch_bounds__(WAVES * 64) void k_rows(GroupedLaunch p) {
+  static_assert(EPI == kEpiSwiglu || EPI == kEpiRows, "Q4 epilogues only");
+  extern __shared__ uint4 s_dyn[];
+  uint8_t* s_a = reinterpret_cast<uint8_t*>(s_dyn);
+  PhaseTrace tr;
+  if (p.trace != nullptr) tr.mark(0);
+  const bool live = rows_item<EPI, WAVES, PROJ, KCH>(p, blockIdx.x, s_a, tr);
+  if (p.trace != nullptr && threadIdx.x == 0) {
+    tr.mark(5);
+    tr.t[7] = live ? 1u : 0u;
+    tr.write(p.trace, EPI == kEpiSwiglu ? 7 : 8, blockIdx.x);
+  }
+}
+
 // ------------------------------------------------------------------ sort ---
 
 // Inclusive scan of one value per thread over a block of 1024 threads.
@@ -642,16 +883,16 @@ __device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
 __device__ uint32_t sort_layout(const SortLaunch& p, uint32_t n, uint32_t* s_wave) {
   const uint32_t g = threadIdx.x;
   const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
-  const uint32_t nt = (n + kGroupedRows - 1) / kGroupedRows;
-  const uint32_t nt_dn = (n + kGroupedRowsDown - 1) / kGroupedRowsDown;
+  const uint32_t nt = (n + p.tile_rows - 1) / p.tile_rows;
+  const uint32_t nt_dn = (n + p.tile_rows_dn - 1) / p.tile_rows_dn;
   const uint32_t row_end = block_scan_1024(n, s_wave);
   const uint32_t tile_end = block_scan_1024(nt, s_wave);
   const uint32_t tile_end_dn = block_scan_1024(nt_dn, s_wave);
   const uint32_t row_begin = row_end - n, tile_begin = tile_end - nt, tile_begin_dn = tile_end_dn - nt_dn;
   if (g < groups) {
     p.row_off[g] = row_begin;
-    for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * kGroupedRows);
-    for (uint32_t i = 0; i < nt_dn; ++i) p.tiles_dn[tile_begin_dn + i] = make_uint2(g, i * kGroupedRowsDown);
+    for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * p.tile_rows);
+    for (uint32_t i = 0; i < nt_dn; ++i) p.tiles_dn[tile_begin_dn + i] = make_uint2(g, i * p.tile_rows_dn);
   }
   if (g == groups - 1) {
     p.row_off[groups] = row_end;
@@ -804,21 +1045,14 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
     }
     return;
   }
-  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (uint32_t j = 0; j < p.slots; ++j) {
-    const uint32_t row = p.pair_row[t * p.slots + j];
-    if (row == kNoRow) continue;
-    const float sc = load_any(p.scores, static_cast<size_t>(t) * p.slots + j, p.score_dtype);
-    const uint4 v = ldg16(p.rows + static_cast<size_t>(row) * p.hidden + h0);
-    const uint32_t words[4] = {v.x, v.y, v.z, v.w};
+  // every load of the token is issued before the sums (slots <= kCombineSlots):
+  // row indices and scores, then the expert rows and the shared row, so the
+  // thread waits for one round trip of each kind rather than one per slot
+  uint32_t row[kCombineSlots];
+  float sc[kCombineSlots];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float d = bf16_to_f32(e & 1 ? words[e / 2] >> 16 : words[e / 2] & 0xffffu);
-      const float prod = __fmul_rn(d, sc);
-      acc[e] = __fadd_rn(acc[e], p.mode == 1 ? round_bf16(prod) : prod);
-    }
-  }
-  uint32_t out[4];
+  for (int j = 0; j < kCombineSlots; ++j)
+    row[j] = j < static_cast<int>(p.slots) ? p.pair_row[t * p.slots + j] : kNoRow;
   uint4 sh = make_uint4(0, 0, 0, 0);
   float sig = 0.0f;
   if (p.shared_first != nullptr) {
@@ -827,6 +1061,25 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
   } else if (p.shared_y != nullptr) {
     sh = ldg16(static_cast<const uint16_t*>(p.shared_y) + static_cast<size_t>(t) * p.hidden + h0);
   }
+  uint4 v[kCombineSlots];
+#pragma unroll
+  for (int j = 0; j < kCombineSlots; ++j) {
+    sc[j] = row[j] != kNoRow ? load_any(p.scores, static_cast<size_t>(t) * p.slots + j, p.score_dtype) : 0.0f;
+    v[j] = row[j] != kNoRow ? ldg16(p.rows + static_cast<size_t>(row[j]) * p.hidden + h0) : make_uint4(0, 0, 0, 0);
+  }
+  float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+  for (int j = 0; j < kCombineSlots; ++j) {
+    if (row[j] == kNoRow) continue;
+    const uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = bf16_to_f32(e & 1 ? words[e / 2] >> 16 : words[e / 2] & 0xffffu);
+      const float prod = __fmul_rn(d, sc[j]);
+      acc[e] = __fadd_rn(acc[e], p.mode == 1 ? round_bf16(prod) : prod);
+    }
+  }
+  uint32_t out[4];
   const uint32_t shw[4] = {sh.x, sh.y, sh.z, sh.w};
 #pragma unroll
   for (int e = 0; e < 8; e += 2) {
@@ -961,6 +1214,64 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
   }
 }
 
+// The k_rows instances: K of 256, 512, 1024, 2048 or 4096 exactly (their
+// strides are compile-time; the A rows of a 16-row tile take 8 to 128 KiB of
+// LDS).  Other K take the chunked GEMM.
+constexpr uint32_t kRowsMaxK = 4096;
+
+bool rows_supported(uint32_t k_dim) {
+  return k_dim == 256 || k_dim == 512 || k_dim == 1024 || k_dim == 2048 || k_dim == kRowsMaxK;
+}
+
+template <int EPI, int WAVES, int PROJ, int KCH>
+hipError_t rows_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  auto kernel = &k_rows<EPI, WAVES, PROJ, KCH>;
+  constexpr uint32_t lds = 16u * KCH * kCG * kGroup * 2u;
+  static bool attr = false;  // one attribute call per kernel instance
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const uint32_t cols = WAVES * 16;
+  const dim3 grid(((p.n_dim + cols - 1) / cols) * ((max_tiles + 7) / 8 * 8));
+  GroupedLaunch q = p;
+  q.trace = trace_reserve(grid.x);
+  hipEvent_t start = nullptr, stop = nullptr;
+  if (timing_events(family, &start, &stop))
+    hipExtLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, start, stop, 0, q);
+  else
+    hipLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, q);
+  return hipGetLastError();
+}
+
+#ifndef VM_ROWS_GU_WAVES
+#define VM_ROWS_GU_WAVES 4
+#endif
+#ifndef VM_ROWS_DN_WAVES
+#define VM_ROWS_DN_WAVES 8
+#endif
+
+template <int EPI, int WAVES, int PROJ>
+hipError_t rows_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  switch (p.k_dim) {
+    case 256: return rows_go_k<EPI, WAVES, PROJ, 1>(family, p, max_tiles, stream);
+    case 512: return rows_go_k<EPI, WAVES, PROJ, 2>(family, p, max_tiles, stream);
+    case 1024: return rows_go_k<EPI, WAVES, PROJ, 4>(family, p, max_tiles, stream);
+    case 2048: return rows_go_k<EPI, WAVES, PROJ, 8>(family, p, max_tiles, stream);
+    case 4096: return rows_go_k<EPI, WAVES, PROJ, 16>(family, p, max_tiles, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_rows(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  if (!rows_supported(p.k_dim)) return hipErrorInvalidValue;
+  if (epi == kEpiSwiglu) return rows_go<kEpiSwiglu, VM_ROWS_GU_WAVES, 2>("grouped_gateup", p, max_tiles, stream);
+  if (epi == kEpiRows) return rows_go<kEpiRows, VM_ROWS_DN_WAVES, 1>("grouped_down", p, max_tiles, stream);
+  return hipErrorInvalidValue;
+}
+
 // Calls up to this many (token, slot) pairs sort in one block.
 constexpr uint32_t kSortOneBlockPairs = 4096;
 
@@ -976,6 +1287,7 @@ hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
 }
 
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {
+  if (p.slots == 0 || p.slots > static_cast<uint32_t>(kCombineSlots)) return hipErrorInvalidValue;
   const uint32_t n = p.tokens * (p.hidden / 8);
   return launch("combine", k_grouped_combine, dim3((n + kGB - 1) / kGB), dim3(kGB), stream, p);
 }

@@ -229,15 +229,16 @@ struct GroupedLaunch {
   const float* bias;           // router, optional [N]
   void* out;
   uint32_t* status;
+  uint64_t* trace;             // phase trace of the 16-row tile kernels (diagnostics), or null
   uint32_t k_dim, n_dim, experts, a_stride;
 };
 
 struct SortLaunch {
   const int32_t* inds;         // [tokens, slots]
   uint32_t* row_off;           // [groups + 1]
-  uint2* tiles;                // kGroupedRows-row tiles (gate/up)
+  uint2* tiles;                // tile_rows-row tiles (gate/up)
   uint32_t* tile_count;
-  uint2* tiles_dn;             // kGroupedRowsDown-row tiles (down)
+  uint2* tiles_dn;             // tile_rows_dn-row tiles (down)
   uint32_t* tile_count_dn;
   uint32_t* counts;            // [1024] scratch of the multi-block sort: rows per group
   uint32_t* cursors;           // [1024] scratch of the multi-block sort: next free row per group
@@ -245,6 +246,7 @@ struct SortLaunch {
   uint32_t* pair_row;          // [tokens * slots]
   uint32_t* status;
   uint32_t tokens, slots, experts, shared_rows;
+  uint32_t tile_rows, tile_rows_dn;  // rows per tile of the two lists
 };
 
 struct CombineLaunch {
@@ -264,6 +266,11 @@ struct CombineLaunch {
 // Upper bound of the tiles of `tile_rows` rows over `groups` groups holding `rows` rows.
 uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups, uint32_t tile_rows);
 hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
+// The 16-row tile kernels of small calls (see k_rows); false when K is above
+// their LDS bound.
+constexpr int kRowsTile = 16;
+bool rows_supported(uint32_t k_dim);
+hipError_t launch_rows(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream);
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream);
 hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
