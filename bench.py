@@ -207,10 +207,40 @@ def grouped_bytes(spec, tokens, distinct):
     return distinct * record + shared + seg + spec.experts * spec.hidden * 2 + 2 * tokens * spec.hidden * 2
 
 
-def run_grouped(name, tokens, layers, reps, seed):
+def scale_router_bias(stack, x, top_k, target_distinct):
+    """Scale every layer's log-Zipf logit bias by one factor, found by
+    bisection so that the calls' mean number of distinct routed experts is
+    `target_distinct` (fp32 logits; distinct counts fall as the bias grows)."""
+    import torch
+
+    base = [layer.gate.bias.clone() for layer in stack]
+
+    def distinct(scale):
+        total = 0
+        for i, layer in enumerate(stack):
+            logits = x[i].float() @ layer.gate.weight.float().T + base[i] * scale
+            total += logits.topk(top_k, dim=1).indices.unique().numel()
+        return total / len(stack)
+
+    lo, hi = 0.0, 1.0
+    for _ in range(24):
+        mid = 0.5 * (lo + hi)
+        if distinct(mid) > target_distinct:
+            lo = mid
+        else:
+            hi = mid
+    scale = 0.5 * (lo + hi)
+    for i, layer in enumerate(stack):
+        layer.gate.bias = (base[i] * scale).contiguous()
+    torch.cuda.synchronize()
+    return scale
+
+
+def run_grouped(name, tokens, layers, reps, seed, target_distinct=None):
     """One grouped workload: layer calls of `tokens` rows cycling over `layers`
     pool-resident layers; wall clock over the timed calls, per-kernel HIP
-    event timing in a second pass."""
+    event timing in a second pass.  `target_distinct`: the logit bias is
+    scaled to route that many distinct experts per call on average."""
     import numpy as np
     import torch
 
@@ -224,6 +254,7 @@ def run_grouped(name, tokens, layers, reps, seed):
     gen = torch.Generator(device=device)
     gen.manual_seed(seed + 1)
     x = torch.randn((layers, tokens, spec.hidden), device=device, generator=gen).to(torch.bfloat16)
+    bias_scale = scale_router_bias(stack, x, spec.top_k, target_distinct) if target_distinct else 1.0
     out = torch.empty_like(x)
     inds = torch.empty((layers, tokens, spec.top_k), dtype=torch.int32, device=device)
     scores = torch.empty((layers, tokens, spec.top_k), dtype=torch.bfloat16, device=device)
@@ -255,11 +286,26 @@ def run_grouped(name, tokens, layers, reps, seed):
     us = elapsed * 1e6 / calls
     nbytes = grouped_bytes(spec, tokens, distinct)
     flops = grouped_flops(spec, tokens)
+    tflops = flops / (us * 1e6)
+    # the bound of the whole call: min(MFMA peak, arithmetic intensity x HBM peak)
+    intensity = flops / nbytes
+    bound_tflops = min(BF16_MFMA_PEAK_TFLOPS, intensity * HBM_PEAK_GBPS / 1e3)
     result = {"tokens": tokens, "tok_s": round(tokens / (us * 1e-6), 1), "us_per_layer": round(us, 2),
               "layers_cycled": layers, "calls": calls, "distinct_experts": round(distinct, 1),
+              "router_bias_scale": round(bias_scale, 4),
               "algorithmic_bytes": int(nbytes), "gbps": round(nbytes / (us * 1e3), 1),
-              "tflops": round(flops / (us * 1e6), 2),
-              "mfma_frac": round(flops / (us * 1e6) / BF16_MFMA_PEAK_TFLOPS, 4),
+              "tflops": round(tflops, 2),
+              "mfma_frac": round(tflops / BF16_MFMA_PEAK_TFLOPS, 4),
+              "flop_per_byte": round(intensity, 1),
+              "bound_tflops": round(bound_tflops, 1),
+              "frac_of_min_mfma_ai_bw": round(tflops / bound_tflops, 4),
+              "roofline": {"bound": "hbm" if bound_tflops < BF16_MFMA_PEAK_TFLOPS else "mfma",
+                           "achieved": round(nbytes / (us * 1e3), 1) if bound_tflops < BF16_MFMA_PEAK_TFLOPS
+                           else round(tflops, 2),
+                           "peak": HBM_PEAK_GBPS if bound_tflops < BF16_MFMA_PEAK_TFLOPS else BF16_MFMA_PEAK_TFLOPS,
+                           "unit": "GB/s" if bound_tflops < BF16_MFMA_PEAK_TFLOPS else "TFLOP/s",
+                           "frac": round(tflops / bound_tflops, 4),
+                           "scope": "whole layer call (every kernel), algorithmic bytes of the routed experts"},
               "kernels_us": kernels}
     del stack, pool, args, refs, x, out, inds, scores
     torch.cuda.empty_cache()
@@ -765,6 +811,8 @@ def main():
     if not args.no_grouped:
         log("batched decode: 32 rows, Zipf(1.1) routing")
         result["batched"] = run_grouped("batched", 32, 8, 50, args.seed)
+        log("batched decode at the distinct-expert count of i.i.d. Zipf(1.1) draws (~133)")
+        result["batched_133_distinct"] = run_grouped("batched", 32, 8, 50, args.seed, target_distinct=133)
         log("chunked prefill: 2048 rows")
         result["prefill"] = run_grouped("prefill", 2048, 3, 8, args.seed)
         log("layer-major prefill window: four 2048-row chunks per layer call")
