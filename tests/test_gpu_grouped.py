@@ -195,11 +195,15 @@ def _switch(np_packs, hidden, inter, experts, device):
 
 
 @pytest.mark.parametrize("mode", [COMBINE_NONE, COMBINE_GENERIC, COMBINE_FUSED])
-@pytest.mark.parametrize("tokens,crowd", [(150, 100), (60, 40)], ids=["64-row-tiles", "16-row-tiles"])
-def test_grouped_experts_modes(device, mode, tokens, crowd):
-    """150 tokens run the 64-row tile GEMM, 60 the 16-row tile kernels; one
-    expert takes `crowd` rows, so it spans two (three) tiles."""
-    hidden, inter, experts, k = 256, 128, 12, 3
+@pytest.mark.parametrize("tokens,crowd,hidden,inter", [(150, 100, 256, 128), (60, 40, 256, 256), (24, 17, 4096, 512)],
+                         ids=["64-row-tiles", "16-row-tiles", "16-row-tiles-k4096"])
+def test_grouped_experts_modes(device, mode, tokens, crowd, hidden, inter):
+    """150 tokens run the 64-row tile GEMM; calls of up to 64 rows whose
+    hidden and intermediate sizes have an instance run the 16-row tile
+    kernels (K = 256 both ways; K = 4096 for gate/up with 512 for down, the
+    largest instance).  One expert takes `crowd` rows, so it spans two
+    (three, two) tiles."""
+    experts, k = 12, 3
     np_packs = packs(41, hidden, inter, experts)
     rng = np.random.default_rng(42)
     inds = np.stack([rng.choice(experts, k, replace=False) for _ in range(tokens)]).astype(np.int32)
