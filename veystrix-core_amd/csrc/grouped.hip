@@ -13,8 +13,9 @@
 //            each XCD takes a contiguous run of the sorted tiles with all their
 //            slices, so the slices of one row tile share its L2 copy of the
 //            tile's A rows and the tiles of one expert share its weights.  K runs in chunks of
-//            eight 32-input groups.  Per chunk the block stages in LDS (double
-//            buffered): the A rows (32 lanes per 512-byte row segment,
+//            eight 32-input groups.  Per chunk the block stages in LDS (one
+//            stage for gate/up, two for down and the router): the A rows (32
+//            lanes per 512-byte row segment,
 //            pair-permuted to match the dequantised weights), the Q4 weight
 //            row chunks (8 lanes per 128-byte line) and the scale and bias
 //            vectors; the 16-byte units of A rows and weight lines are
@@ -461,31 +462,51 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   };
   // only a K that is not a multiple of the chunk has a tail chunk
   auto tail_chunk = [&](uint32_t c) { return TAIL && (c + 1) * kCG > G; };
-  // Loads run one chunk ahead.  The copy of the next chunk's B registers
-  // makes the end of a chunk wait for them; an unrolled ping-pong without
-  // that wait, and a third register set, both measured slower here.
-  a_load(0, tail_chunk(0));
-  if constexpr (!kLdsB) b_load(b0, 0, tail_chunk(0));
-  a_store(0);
-  __syncthreads();
-  for (uint32_t c = 0; c < chunks; ++c) {
-    const int buf = c & 1;
-    const bool more = c + 1 < chunks;
-    if (more) {
-      a_load((c + 1) * kCG, tail_chunk(c + 1));
-      if constexpr (!kLdsB) b_load(b1, (c + 1) * kCG, tail_chunk(c + 1));
+  // Loads run one chunk ahead.  With staged weights (gate/up) there is one
+  // LDS stage: the next chunk waits in registers while this one is computed
+  // and a second barrier guards its store.  Half the LDS of a double buffer
+  // lets two 4-wave blocks share a CU, whose barriers then do not hold each
+  // other up (gate/up at 2048 rows 258 -> 237 us against one 8-wave block
+  // with two stages; 700 -> 651 us at 8192).  Without staged weights (down,
+  // router) the two-stage ping-pong stays: the copy of the next chunk's B
+  // registers makes the end of a chunk wait for them; an unrolled ping-pong
+  // without that wait, and a third register set, both measured slower.
+  if constexpr (kLdsB) {
+    a_load(0, tail_chunk(0));
+    a_store(0);
+    __syncthreads();
+    for (uint32_t c = 0; c < chunks; ++c) {
+      const bool more = c + 1 < chunks;
+      if (more) a_load((c + 1) * kCG, tail_chunk(c + 1));
+      compute(0, b0);
+      __syncthreads();
+      if (more) {
+        a_store(0);
+        __syncthreads();
+      }
     }
-    compute(buf, b0);
-    if (more) {
-      a_store(buf ^ 1);
-      if constexpr (!kLdsB) {
+  } else {
+    a_load(0, tail_chunk(0));
+    b_load(b0, 0, tail_chunk(0));
+    a_store(0);
+    __syncthreads();
+    for (uint32_t c = 0; c < chunks; ++c) {
+      const int buf = c & 1;
+      const bool more = c + 1 < chunks;
+      if (more) {
+        a_load((c + 1) * kCG, tail_chunk(c + 1));
+        b_load(b1, (c + 1) * kCG, tail_chunk(c + 1));
+      }
+      compute(buf, b0);
+      if (more) {
+        a_store(buf ^ 1);
 #pragma unroll
         for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
           for (int nb = 0; nb < NBW; ++nb) b0[pj][nb] = b1[pj][nb];
       }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // epilogue: lane holds rows 4*(lane/16) + i of every row block, column lane%16
@@ -1160,7 +1181,8 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
 
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
 hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
-  constexpr uint32_t lds = 2 * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
+  // one LDS stage with staged weights (see grouped_tile), else two
+  constexpr uint32_t lds = (lds_weights<EPI, TAIL>() ? 1 : 2) * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
   auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL>;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
@@ -1193,7 +1215,7 @@ uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups, uint32_t tile_rows) {
 
 // block shapes (waves, 16-column blocks per wave) of the gate/up and down GEMMs
 #ifndef VM_GU_WAVES
-#define VM_GU_WAVES 8
+#define VM_GU_WAVES 4
 #endif
 #ifndef VM_GU_NBW
 #define VM_GU_NBW 1
