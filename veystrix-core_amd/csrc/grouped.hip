@@ -14,7 +14,7 @@
 //            slices, so the slices of one row tile share its L2 copy of the
 //            tile's A rows and the tiles of one expert share its weights.  K runs in chunks of
 //            eight 32-input groups.  Per chunk the block stages in LDS (one
-//            stage for gate/up, two for down and the router): the A rows (32
+//            stage for the Q4 GEMMs, two for the router): the A rows (32
 //            lanes per 512-byte row segment,
 //            pair-permuted to match the dequantised weights), the Q4 weight
 //            row chunks (8 lanes per 128-byte line) and the scale and bias
@@ -85,10 +85,12 @@ __device__ __forceinline__ constexpr uint32_t w_swz(uint32_t c) { return c & 7u;
 #ifndef VM_LDS_B
 #define VM_LDS_B 1
 #endif
-// the down GEMM (K = the intermediate size, two chunks) loads its weights
-// straight into the MFMA lanes: without the weight stage two blocks fit per CU
+// the down GEMM (K = the intermediate size, two chunks) stages its weights too:
+// with one LDS stage (grouped_tile) two blocks still fit per CU, and the
+// coalesced line loads beat loads straight into the MFMA lanes (2048 rows
+// 124 -> 119 us, 8192 rows 377 -> 364 us)
 #ifndef VM_LDS_B_DN
-#define VM_LDS_B_DN 0
+#define VM_LDS_B_DN 1
 #endif
 constexpr int kWColBytes = kCG * 16;  // LDS bytes per staged weight row chunk (unpadded: the groups are swizzled)
 
@@ -462,13 +464,13 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   };
   // only a K that is not a multiple of the chunk has a tail chunk
   auto tail_chunk = [&](uint32_t c) { return TAIL && (c + 1) * kCG > G; };
-  // Loads run one chunk ahead.  With staged weights (gate/up) there is one
+  // Loads run one chunk ahead.  With staged weights (gate/up, down) there is one
   // LDS stage: the next chunk waits in registers while this one is computed
   // and a second barrier guards its store.  Half the LDS of a double buffer
   // lets two 4-wave blocks share a CU, whose barriers then do not hold each
   // other up (gate/up at 2048 rows 258 -> 237 us against one 8-wave block
-  // with two stages; 700 -> 651 us at 8192).  Without staged weights (down,
-  // router) the two-stage ping-pong stays: the copy of the next chunk's B
+  // with two stages; 700 -> 651 us at 8192).  Without staged weights (the
+  // router, tail chunks) the two-stage ping-pong stays: the copy of the next chunk's B
   // registers makes the end of a chunk wait for them; an unrolled ping-pong
   // without that wait, and a third register set, both measured slower.
   if constexpr (kLdsB) {
