@@ -994,6 +994,10 @@ struct GroupedExperts {
 };
 
 static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char* ws, hipStream_t stream) {
+  // the chunked GEMM addresses its activation matrices with 32-bit byte offsets
+  const uint64_t sorted_rows = uint64_t(g.T) * g.K + (g.shared ? g.T : 0);
+  if (uint64_t(g.T) * g.H * 2 > 0xffffffffull || sorted_rows * g.I * 2 > 0xffffffffull)
+    return fail(VM_EUNSUPPORTED, "grouped call of %u tokens: an activation matrix of 4 GiB or more", g.T);
   vm::SortLaunch s{};
   s.inds = g.inds;
   s.row_off = reinterpret_cast<uint32_t*>(ws + w.row_off);
@@ -1038,6 +1042,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.k_dim = g.H;
   q.n_dim = g.I;
   q.a_stride = g.H;
+  q.a_rows = g.T;
   e = w.small ? vm::launch_rows(vm::kEpiSwiglu, q, w.max_tiles, stream)
               : vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped gate/up launch");
@@ -1053,6 +1058,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.k_dim = g.I;
   q.n_dim = g.H;
   q.a_stride = g.I;
+  q.a_rows = g.T * g.K + (g.shared ? g.T : 0);
   q.tiles = s.tiles_dn;
   q.tile_count = s.tile_count_dn;
   e = w.small ? vm::launch_rows(vm::kEpiRows, q, w.max_tiles_dn, stream)
@@ -1119,6 +1125,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     r.k_dim = H;
     r.n_dim = E;
     r.a_stride = H;
+    r.a_rows = T;
     r.experts = E;
     e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
     if (e != hipSuccess) return hip_fail(e, "router launch");

@@ -285,19 +285,32 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   // it % kUnits of the chunk): 32 consecutive lanes read one row's 512
   // contiguous bytes, so a wave's load covers whole cache lines.  Rows past
   // the tile repeat its first row: an MFMA output row depends on its own A
-  // row only, and those rows are not stored.
-  uint32_t a_off[kItems], a_u[kItems];
-  const uint16_t* a_src[kItems];
+  // row only, and those rows are not stored.  Every global load of the loop
+  // is a wave-uniform base (SGPRs, advanced per chunk by scalar adds) plus a
+  // 32-bit byte offset per lane: one VGPR per address and no 64-bit address
+  // arithmetic per chunk (launch_grouped keeps the A matrix under 4 GiB).
+  static_assert(kThreads % kUnits == 0, "an item step covers whole rows");
+  constexpr int kRS = kThreads / kUnits;  // rows per item step
+  const uint32_t a_u = tid % kUnits;      // the thread's 16-byte unit, the same for every item
+  uint32_t a_vo[kItems];
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
-    const uint32_t it = tid + j * kThreads;
-    const uint32_t r = it / kUnits, u = it % kUnits;
+    const uint32_t r = tid / kUnits + kRS * j;
     const uint32_t rr = r < rows ? r : 0u;
     const uint32_t arow = p.row_token != nullptr ? p.row_token[row0 + rr] : row0 + rr;
-    a_src[j] = p.a + static_cast<size_t>(arow) * p.a_stride + u * 8;
-    a_u[j] = u;
-    a_off[j] = r * kRowB + (u ^ (kSwz ? a_swz(r) : 0u)) * 16;
+    a_vo[j] = (arow * p.a_stride + a_u * 8) * 2u;
   }
+  // LDS offset of item j: the swizzle depends on the row mod 16, so it
+  // repeats every kP items and the rest of the offset is an immediate
+  constexpr int kP = !kSwz || kRS % 16 == 0 ? 1 : kRS % 8 == 0 ? 2 : kRS % 4 == 0 ? 4 : kRS % 2 == 0 ? 8 : 16;
+  constexpr int kPA = kP < kItems ? kP : kItems;
+  uint32_t a_off0[kPA];
+#pragma unroll
+  for (int j = 0; j < kPA; ++j) {
+    const uint32_t r = tid / kUnits + kRS * j;
+    a_off0[j] = r * kRowB + (a_u ^ (kSwz ? a_swz(r) : 0u)) * 16;
+  }
+  auto a_off = [&](int j) { return a_off0[j % kPA] + (j / kPA) * (kPA * kRS * kRowB); };
   // scale staging (Q4, full chunks): vector v = tid + j * threads -> (proj,
   // scales or biases, column of the block); 16 bytes = the chunk's 8 groups
   constexpr int kCols = WAVES * NBW * 16;
@@ -306,7 +319,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr int kSItems = (kSVecs + kThreads - 1) / kThreads;
   constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
   constexpr int kStageBytes = tile_rows<EPI>() * kRowB;  // the A rows of a stage
-  const uint16_t* sv_src[kSItems > 0 ? kSItems : 1];
+  const uint8_t* sv_base[kSItems > 0 ? kSItems : 1];  // wave-uniform
+  uint32_t sv_vo[kSItems > 0 ? kSItems : 1];
 #pragma unroll
   for (int j = 0; j < kSItems; ++j) {
     static_assert(kCols % 64 == 0, "a wave's vectors share one (projection, scales or biases)");
@@ -320,8 +334,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     VM_KEEP(pb0);
     VM_KEEP(ps1);
     VM_KEEP(pb1);
-    const uint16_t* base = q >= 2 ? ((q & 1u) ? pb1 : ps1) : ((q & 1u) ? pb0 : ps0);
-    sv_src[j] = base + static_cast<size_t>(col) * G;
+    sv_base[j] = reinterpret_cast<const uint8_t*>(q >= 2 ? ((q & 1u) ? pb1 : ps1) : ((q & 1u) ? pb0 : ps0));
+    sv_vo[j] = col * G * 2u;
   }
   // weight staging (lds_weights): item it = tid + j * threads -> (projection,
   // column of the block, group of the chunk); eight lanes read one row's
@@ -331,31 +345,40 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr int kWItems = kWVecs / kThreads;
   constexpr int kWArea = kStageBytes + (kLdsScales ? PROJ * 2 * kCols * 16 : 0);
   static_assert(!kLdsB || (kWVecs % kThreads == 0 && (kCols * kCG) % kThreads == 0), "whole items per thread");
-  const uint8_t* w_src[kWItems > 0 ? kWItems : 1];
+  uint32_t w_vo[kWItems > 0 ? kWItems : 1];  // byte offsets from the projection's weights
   uint32_t w_off[kWItems > 0 ? kWItems : 1];
 #pragma unroll
   for (int j = 0; j < kWItems; ++j) {
     constexpr int kPerProj = kCols * kCG;
     const uint32_t it = tid + j * kThreads;
-    const int pj = (j * kThreads) / kPerProj;  // compile-time
     const uint32_t ci = (it % kPerProj) / kCG, g = it % kCG;
     const uint32_t col = min(slice * kCols + ci, N - 1);
-    w_src[j] = reinterpret_cast<const uint8_t*>(w[pj].w) + static_cast<size_t>(col) * (K / 2) + g * 16u;
-    w_off[j] = kWArea + (pj * kCols + ci) * kWColBytes + (g ^ w_swz(ci)) * 16u;
+    w_vo[j] = col * (K / 2) + g * 16u;
+    w_off[j] = kWArea + ((j * kThreads) / kPerProj * kCols + ci) * kWColBytes + (g ^ w_swz(ci)) * 16u;
   }
   uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1], wr[kWItems > 0 ? kWItems : 1];
+  // The offsets pass through an empty asm so that loop strength reduction
+  // does not turn them back into one 64-bit pointer per load.
+  auto opaque = [](uint32_t v) {
+    asm volatile("" : "+v"(v));
+    return v;
+  };
   auto a_load = [&](uint32_t g0, bool tail) {
+    const uint8_t* ab = reinterpret_cast<const uint8_t*>(p.a) + g0 * (kGroup * 2u);
+    const bool zero = tail && g0 + a_u / 4 >= G;  // the thread's unit is past K
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
       if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
-      const uint16_t* src = a_src[j] + g0 * kGroup;
-      if (tail && g0 + a_u[j] / 4 >= G) src = reinterpret_cast<const uint16_t*>(g_zero_page);
-      ar[j] = ldg16(src);
+      ar[j] = ldg16(TAIL && zero ? reinterpret_cast<const uint8_t*>(g_zero_page) : ab + opaque(a_vo[j]));
     }
 #pragma unroll
-    for (int j = 0; j < kSItems; ++j) sr[j] = ldg16(sv_src[j] + g0);
+    for (int j = 0; j < kSItems; ++j) sr[j] = ldg16(sv_base[j] + g0 * 2u + opaque(sv_vo[j]));
 #pragma unroll
-    for (int j = 0; j < kWItems; ++j) wr[j] = ldg16(w_src[j] + g0 * 16u);
+    for (int j = 0; j < kWItems; ++j) {
+      constexpr int kPerProj = kCols * kCG;
+      const int pj = (j * kThreads) / kPerProj;  // compile-time
+      wr[j] = ldg16(reinterpret_cast<const uint8_t*>(w[pj].w) + g0 * 16u + opaque(w_vo[j]));
+    }
   };
   // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
   auto pair_perm = [](const uint4 v) {
@@ -366,7 +389,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
       if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
-      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + a_off[j]) = pair_perm(ar[j]);
+      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + a_off(j)) = pair_perm(ar[j]);
     }
 #pragma unroll
     for (int j = 0; j < kSItems; ++j) {
@@ -467,9 +490,10 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   // Loads run one chunk ahead.  With staged weights (gate/up, down) there is one
   // LDS stage: the next chunk waits in registers while this one is computed
   // and a second barrier guards its store.  Half the LDS of a double buffer
-  // lets two 4-wave blocks share a CU, whose barriers then do not hold each
-  // other up (gate/up at 2048 rows 258 -> 237 us against one 8-wave block
-  // with two stages; 700 -> 651 us at 8192).  Without staged weights (the
+  // lets several 4-wave blocks share a CU, whose barriers then do not hold
+  // each other up (gate/up at 2048 rows 258 -> 237 us against one 8-wave
+  // block with two stages; 700 -> 651 us at 8192; with the 32-bit load
+  // offsets three blocks fit, 232 -> 208 us and 660 -> 586 us).  Without staged weights (the
   // router, tail chunks) the two-stage ping-pong stays: the copy of the next chunk's B
   // registers makes the end of a chunk wait for them; an unrolled ping-pong
   // without that wait, and a third register set, both measured slower.
@@ -1230,6 +1254,11 @@ uint32_t grouped_max_tiles(uint32_t rows, uint32_t groups, uint32_t tile_rows) {
 #endif
 
 hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  // the kernels address A, and each projection's weights, scales and biases,
+  // with 32-bit byte offsets
+  if (p.a_rows == 0 || static_cast<uint64_t>(p.a_rows) * p.a_stride * 2u > 0xffffffffull ||
+      static_cast<uint64_t>(p.n_dim) * p.k_dim > 0xffffffffull)
+    return hipErrorInvalidValue;
   switch (epi) {
     case kEpiSwiglu:
       return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>("grouped_gateup", p, max_tiles, stream);
