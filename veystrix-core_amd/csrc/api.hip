@@ -183,6 +183,45 @@ int scratch_address(void** out) {
   return VM_OK;
 }
 
+// A second stream of the calling thread on the current device, for the part
+// of a grouped layer call that does not depend on the routing (the shared
+// expert): forked from the caller's stream with one event and joined back
+// with another before the combine, so it runs beside the router GEMM, the
+// selection and the sort, which leave most of the GPU idle.  Created on the
+// thread's first such call on the device (never while the caller's stream is
+// being captured, and never for vm_moe_layer_static, whose callers cannot
+// allocate) and held until the process ends.  Without it the call takes the
+// one-stream path, with the same results.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+thread_local bool t_static_call = false;
+
+SideStream* side_stream(hipStream_t caller) {
+  thread_local SideStream per_device[kMaxDevices];
+  if (t_static_call) return nullptr;
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  SideStream& s = per_device[dev];
+  if (s.stream == nullptr) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(caller, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return nullptr;
+    SideStream n;
+    if (hipStreamCreateWithFlags(&n.stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&n.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&n.join, hipEventDisableTiming) != hipSuccess) {
+      if (n.join != nullptr) (void)hipEventDestroy(n.join);
+      if (n.fork != nullptr) (void)hipEventDestroy(n.fork);
+      if (n.stream != nullptr) (void)hipStreamDestroy(n.stream);
+      (void)hipGetLastError();
+      return nullptr;
+    }
+    s = n;
+  }
+  return &s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -637,7 +676,10 @@ int vm_moe_layer_static(const VmLayerArgs* a, void* stream_ptr) {
   VmLayerArgs c = *a;
   c.workspace = ptr;
   c.workspace_bytes = VM_STATIC_SCRATCH_BYTES;
-  return vm_moe_layer(&c, stream_ptr);
+  t_static_call = true;
+  rc = vm_moe_layer(&c, stream_ptr);
+  t_static_call = false;
+  return rc;
 }
 
 // Router logits (and the shared expert's sigmoid gate) of a decode call.
@@ -986,6 +1028,10 @@ struct GroupedExperts {
   VmQ4Proj shared_gate, shared_up, shared_down;
   const void* sig;
   const void* shared_y;
+  // the shared expert ran on the side stream: its output rows, and the event
+  // the combine waits for (shared is then false for the sort and the GEMMs)
+  const uint16_t* shared_rows;
+  hipEvent_t shared_join;
   void* output;
   vm::Inject inject;
   uint32_t* status;
@@ -1073,6 +1119,11 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   if (g.shared) {
     c.shared_first = s.row_off + g.E;
     c.shared_sig = g.sig;
+  } else if (g.shared_rows != nullptr) {
+    c.shared_rows = g.shared_rows;
+    c.shared_sig = g.sig;
+    e = hipStreamWaitEvent(stream, g.shared_join, 0);
+    if (e != hipSuccess) return hip_fail(e, "join of the shared expert's stream");
   }
   c.shared_y = g.shared_y;
   c.out = g.output;
@@ -1084,6 +1135,42 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   e = vm::launch_grouped_combine(c, stream);
   if (e != hipSuccess) return hip_fail(e, "combine launch");
   return VM_OK;
+}
+
+// The shared expert of a grouped call over all T rows, with no sort: its
+// sigmoid gate into sig, gate/up + SwiGLU into sh_act [T, I] and down into
+// sh_rows [T, H] (one-group launches of the chunked GEMM).
+static hipError_t launch_shared_expert(const VmLayerArgs* a, uint16_t* sig, uint16_t* sh_act, uint16_t* sh_rows,
+                                       hipStream_t stream) {
+  const uint32_t T = a->tokens, H = a->hidden_size, I = a->inter_size;
+  hipError_t e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T,
+                                        H, stream);
+  if (e != hipSuccess) return e;
+  vm::GroupedLaunch q{};
+  q.a = static_cast<const uint16_t*>(a->x);
+  q.rows = T;
+  q.experts = 0;  // every tile is the shared expert's
+  q.shared[0] = to_ptrs(a->shared_gate_proj);
+  q.shared[1] = to_ptrs(a->shared_up_proj);
+  q.part[0] = 0;
+  q.part[1] = 1;
+  q.out = sh_act;
+  q.status = a->status;
+  q.k_dim = H;
+  q.n_dim = I;
+  q.a_stride = H;
+  q.a_rows = T;
+  e = vm::launch_grouped(vm::kEpiSwiglu, q, (T + vm::kGroupedRows - 1) / vm::kGroupedRows, stream);
+  if (e != hipSuccess) return e;
+  q.a = sh_act;
+  q.shared[0] = to_ptrs(a->shared_down_proj);
+  q.shared[1] = vm::ProjPtrs{};
+  q.part[0] = 2;
+  q.out = sh_rows;
+  q.k_dim = I;
+  q.n_dim = H;
+  q.a_stride = I;
+  return vm::launch_grouped(vm::kEpiRows, q, (T + vm::kGroupedRowsDown - 1) / vm::kGroupedRowsDown, stream);
 }
 
 static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
@@ -1099,6 +1186,31 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   uint16_t* sig = reinterpret_cast<uint16_t*>(ws + w.sig);
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   hipError_t e = hipSuccess;
+  // Calls that take the router GEMM run the shared expert on the side stream,
+  // into the last T rows of the activation and expert-row buffers (the routed
+  // rows take at most the first T * K).
+  SideStream* side = nullptr;
+  if (shared && T > kFrontMaxTokens && (phases & VM_PHASE_ROUTER) && (phases & VM_PHASE_EXPERTS))
+    side = side_stream(stream);
+  uint16_t* sh_rows = reinterpret_cast<uint16_t*>(ws + w.rows) + uint64_t(T) * K * H;
+  if (side != nullptr) {
+    e = hipEventRecord(side->fork, stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
+    if (e != hipSuccess) return hip_fail(e, "fork of the shared expert's stream");
+    e = launch_shared_expert(a, sig, reinterpret_cast<uint16_t*>(ws + w.act) + uint64_t(T) * K * I, sh_rows,
+                             side->stream);
+    const hipError_t j = hipEventRecord(side->join, side->stream);
+    if (e != hipSuccess || j != hipSuccess) {
+      if (j == hipSuccess) (void)hipStreamWaitEvent(stream, side->join, 0);
+      return hip_fail(e != hipSuccess ? e : j, "shared expert launch");
+    }
+  }
+  // a failure after the fork still joins the side stream (a capture must not
+  // end with it forked); on success the combine has joined it
+  auto done = [&](int rc) {
+    if (side != nullptr && rc != VM_OK) (void)hipStreamWaitEvent(stream, side->join, 0);
+    return rc;
+  };
   if ((phases & VM_PHASE_ROUTER) && T <= kFrontMaxTokens) {
     // few rows: the decode router (one row per wave, every token) and shared gate
     vm::FrontLaunch f{};
@@ -1113,7 +1225,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     f.experts = E;
     f.act_dtype = VM_BF16;
     e = vm::launch_front(f, stream);
-    if (e != hipSuccess) return hip_fail(e, "router launch");
+    if (e != hipSuccess) return done(hip_fail(e, "router launch"));
   } else if (phases & VM_PHASE_ROUTER) {
     // router logits as an MFMA GEMM over all rows
     vm::GroupedLaunch r{};
@@ -1128,11 +1240,11 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     r.a_rows = T;
     r.experts = E;
     e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
-    if (e != hipSuccess) return hip_fail(e, "router launch");
-    if (shared) {
+    if (e != hipSuccess) return done(hip_fail(e, "router launch"));
+    if (shared && side == nullptr) {
       e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T, H,
                                  stream);
-      if (e != hipSuccess) return hip_fail(e, "shared gate launch");
+      if (e != hipSuccess) return done(hip_fail(e, "shared gate launch"));
     }
   }
   if (phases & VM_PHASE_ROUTER) {
@@ -1147,7 +1259,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     s.act_dtype = VM_BF16;
     s.blend = a->renorm_blend;
     e = vm::launch_select(s, stream);
-    if (e != hipSuccess) return hip_fail(e, "select launch");
+    if (e != hipSuccess) return done(hip_fail(e, "select launch"));
   }
   if (!(phases & VM_PHASE_EXPERTS)) return VM_OK;
   GroupedExperts g{};
@@ -1159,11 +1271,15 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   g.down = a->down;
   g.pool = a->pool;
   g.slot_table = a->slot_table;
-  g.shared = shared;
+  g.shared = shared && side == nullptr;
   g.shared_gate = a->shared_gate_proj;
   g.shared_up = a->shared_up_proj;
   g.shared_down = a->shared_down_proj;
   g.sig = sig;
+  if (side != nullptr) {
+    g.shared_rows = sh_rows;
+    g.shared_join = side->join;
+  }
   g.output = a->output;
   g.inject = to_inject(a);
   g.status = a->status;
@@ -1173,7 +1289,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   g.I = I;
   g.E = E;
   g.mode = 1;  // rows > 8: the reference's generic combine
-  return run_grouped_experts(g, w, ws, stream);
+  return done(run_grouped_experts(g, w, ws, stream));
 }
 
 uint64_t vm_moe_grouped_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,

@@ -1102,8 +1102,10 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
     row[j] = j < static_cast<int>(p.slots) ? p.pair_row[t * p.slots + j] : kNoRow;
   uint4 sh = make_uint4(0, 0, 0, 0);
   float sig = 0.0f;
-  if (p.shared_first != nullptr) {
-    sh = ldg16(p.rows + (static_cast<size_t>(*p.shared_first) + t) * p.hidden + h0);
+  const uint16_t* shr =
+      p.shared_first != nullptr ? p.rows + static_cast<size_t>(*p.shared_first) * p.hidden : p.shared_rows;
+  if (shr != nullptr) {
+    sh = ldg16(shr + static_cast<size_t>(t) * p.hidden + h0);
     sig = ActBF16::load(p.shared_sig, t);
   } else if (p.shared_y != nullptr) {
     sh = ldg16(static_cast<const uint16_t*>(p.shared_y) + static_cast<size_t>(t) * p.hidden + h0);
@@ -1135,7 +1137,7 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
     for (int k = 0; k < 2; ++k) {
       float v = round_bf16(acc[e + k]);
       const float s = bf16_to_f32(k ? shw[e / 2] >> 16 : shw[e / 2] & 0xffffu);
-      if (p.shared_first != nullptr) v = round_bf16(__fadd_rn(v, round_bf16(__fmul_rn(sig, s))));
+      if (shr != nullptr) v = round_bf16(__fadd_rn(v, round_bf16(__fmul_rn(sig, s))));
       else if (p.shared_y != nullptr) v = round_bf16(__fadd_rn(v, s));
       y[k] = v;
     }

@@ -256,6 +256,7 @@ struct CombineLaunch {
   const void* scores;          // [tokens, slots]
   int score_dtype;
   const uint32_t* shared_first; // row of token 0's shared expert output in `rows` (with shared_sig)
+  const uint16_t* shared_rows; // or the shared expert's output rows [tokens, hidden] bf16 (with shared_sig)
   const void* shared_sig;      // [tokens] bf16
   const void* shared_y;        // or a finished shared term [tokens, hidden] bf16
   void* out;                   // [tokens, hidden] bf16
