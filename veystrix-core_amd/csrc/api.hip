@@ -1040,9 +1040,11 @@ struct GroupedExperts {
 };
 
 static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char* ws, hipStream_t stream) {
-  // the chunked GEMM addresses its activation matrices with 32-bit byte offsets
-  const uint64_t sorted_rows = uint64_t(g.T) * g.K + (g.shared ? g.T : 0);
-  if (uint64_t(g.T) * g.H * 2 > 0xffffffffull || sorted_rows * g.I * 2 > 0xffffffffull)
+  // the chunked GEMM addresses its activation matrices with 32-bit byte
+  // offsets and its outputs with 32-bit element indices
+  const uint64_t sorted_rows = uint64_t(g.T) * g.K + g.T;
+  if (uint64_t(g.T) * g.H * 2 > 0xffffffffull || sorted_rows * g.I * 2 > 0xffffffffull ||
+      sorted_rows * g.H > 0xffffffffull)
     return fail(VM_EUNSUPPORTED, "grouped call of %u tokens: an activation matrix of 4 GiB or more", g.T);
   vm::SortLaunch s{};
   s.inds = g.inds;
@@ -1227,7 +1229,9 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     e = vm::launch_front(f, stream);
     if (e != hipSuccess) return done(hip_fail(e, "router launch"));
   } else if (phases & VM_PHASE_ROUTER) {
-    // router logits as an MFMA GEMM over all rows
+    // router logits as an MFMA GEMM over all rows (32-bit output indices)
+    if (uint64_t(T) * E > 0xffffffffull || uint64_t(T) * H * 2 > 0xffffffffull)
+      return done(fail(VM_EUNSUPPORTED, "grouped call of %u tokens: the router GEMM's matrices are too large", T));
     vm::GroupedLaunch r{};
     r.a = static_cast<const uint16_t*>(a->x);
     r.rows = T;

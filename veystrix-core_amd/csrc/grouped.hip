@@ -259,13 +259,31 @@ struct BChunk<false, TAIL> {
   }
 };
 
+// Column slices per block of the one-stage GEMMs (a power of two; the
+// launch halves it until it divides the call's slices).  The down GEMM's
+// blocks are short (two K chunks), so their fixed part (tile lookups, the
+// first chunk's loads, the epilogue) weighed half of each block; with two
+// slices per block the second slice's first loads overlap the first's last
+// chunk.  The gate/up GEMM keeps one: the loop state that the epilogue then
+// keeps live costs its third block per CU (176 VGPRs).
+#ifndef VM_GU_SPB
+#define VM_GU_SPB 1
+#endif
+#ifndef VM_DN_SPB
+#define VM_DN_SPB 2
+#endif
+template <int EPI>
+constexpr uint32_t slices_per_block() {
+  return EPI == kEpiSwiglu ? VM_GU_SPB : EPI == kEpiRows ? VM_DN_SPB : 1;
+}
+
 // The tile body for MBU 16-row blocks in use (rows <= 16 * MBU): the A
 // staging covers those rows only and the MFMA loops carry no branch, so the
 // LDS reads of a step and the MFMAs of neighbouring steps can be scheduled
 // freely.
 template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU>
 __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjPtrs (&w)[PROJ], uint32_t row0,
-                                             uint32_t rows, uint32_t slice, uint8_t* s_a0) {
+                                             uint32_t rows, uint32_t slice0, uint32_t nslices, uint8_t* s_a0) {
   constexpr bool Q4 = EPI != kEpiLogits;
   constexpr int kThreads = WAVES * 64;
   constexpr int kUnits = kCG * 4;                                // 16-byte A units per row and chunk
@@ -279,7 +297,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   const uint32_t lane = tid & 63u;
   const uint32_t wave = tid >> 6;
   const uint32_t K = p.k_dim, N = p.n_dim, G = K / kGroup;
-  const uint32_t n_wave = (slice * WAVES + wave) * NBW * 16;
+  uint32_t slice = slice0;  // the slice being computed (the weights' offsets may already be the next one's)
+  const uint32_t n_wave = (slice0 * WAVES + wave) * NBW * 16;  // B lanes of the two-stage path (one slice)
 
   // A staging: unit it = tid + j * threads -> (row it / kUnits, 16-byte unit
   // it % kUnits of the chunk): 32 consecutive lanes read one row's 512
@@ -328,7 +347,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     // (projection, scales or biases) is wave-uniform: select it in SGPRs (an
     // indexed private array of pointers would go to scratch)
     const uint32_t q = __builtin_amdgcn_readfirstlane(v / kCols);
-    const uint32_t col = min(slice * kCols + v % kCols, N - 1);
+    const uint32_t col = min(slice0 * kCols + v % kCols, N - 1);
     const uint16_t *ps0 = w[0].s, *pb0 = w[0].b, *ps1 = w[PROJ - 1].s, *pb1 = w[PROJ - 1].b;
     VM_KEEP(ps0);  // opaque copies: a select of loads from `w` would become an indexed load
     VM_KEEP(pb0);
@@ -352,10 +371,19 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     constexpr int kPerProj = kCols * kCG;
     const uint32_t it = tid + j * kThreads;
     const uint32_t ci = (it % kPerProj) / kCG, g = it % kCG;
-    const uint32_t col = min(slice * kCols + ci, N - 1);
+    const uint32_t col = min(slice0 * kCols + ci, N - 1);
     w_vo[j] = col * (K / 2) + g * 16u;
     w_off[j] = kWArea + ((j * kThreads) / kPerProj * kCols + ci) * kWColBytes + (g ^ w_swz(ci)) * 16u;
   }
+  // the weight and scale offsets move on to the next slice (the A rows stay);
+  // blocks of several slices have N a multiple of the block's columns, so no
+  // column is clamped
+  auto next_slice = [&]() {
+#pragma unroll
+    for (int j = 0; j < kSItems; ++j) sv_vo[j] += kCols * G * 2u;
+#pragma unroll
+    for (int j = 0; j < kWItems; ++j) w_vo[j] += kCols * (K / 2);
+  };
   uint4 ar[kItems], sr[kSItems > 0 ? kSItems : 1], wr[kWItems > 0 ? kWItems : 1];
   // The offsets pass through an empty asm so that loop strength reduction
   // does not turn them back into one 64-bit pointer per load.
@@ -487,28 +515,94 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   };
   // only a K that is not a multiple of the chunk has a tail chunk
   auto tail_chunk = [&](uint32_t c) { return TAIL && (c + 1) * kCG > G; };
+  // epilogue of slice s: lane holds rows 4*(lane/16) + i of every row block, column lane%16
+  auto epilogue = [&](uint32_t s) {
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+      const uint32_t col = (s * WAVES + wave) * NBW * 16 + nb * 16 + bn;
+      if (col >= N) continue;
+#pragma unroll
+      for (int mb = 0; mb < MBU; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t r = mb * 16 + 4 * bkb + i;
+          if (r >= rows) continue;
+          const uint32_t o = (row0 + r) * N + col;  // outputs stay below 2^32 elements (host checks)
+          if constexpr (EPI == kEpiSwiglu) {
+            const float gv = round_bf16(acc[0][nb][mb][i]);
+            const float uv = round_bf16(acc[PROJ - 1][nb][mb][i]);
+            ActBF16::store(p.out, o, swiglu_act<ActBF16>(gv, uv));
+          } else if constexpr (EPI == kEpiRows) {
+            ActBF16::store(p.out, o, round_bf16(acc[0][nb][mb][i]));
+          } else {
+            float v = acc[0][nb][mb][i];
+            if (p.bias != nullptr) v += p.bias[col];
+            static_cast<float*>(p.out)[o] = round_bf16(v);
+          }
+        }
+      }
+    }
+  };
+
   // Loads run one chunk ahead.  With staged weights (gate/up, down) there is one
   // LDS stage: the next chunk waits in registers while this one is computed
   // and a second barrier guards its store.  Half the LDS of a double buffer
   // lets several 4-wave blocks share a CU, whose barriers then do not hold
   // each other up (gate/up at 2048 rows 258 -> 237 us against one 8-wave
   // block with two stages; 700 -> 651 us at 8192; with the 32-bit load
-  // offsets three blocks fit, 232 -> 208 us and 660 -> 586 us).  Without staged weights (the
-  // router, tail chunks) the two-stage ping-pong stays: the copy of the next chunk's B
-  // registers makes the end of a chunk wait for them; an unrolled ping-pong
-  // without that wait, and a third register set, both measured slower.
+  // offsets three blocks fit, 232 -> 208 us and 660 -> 586 us).  Without
+  // staged weights (the router, tail chunks) the two-stage ping-pong stays:
+  // the copy of the next chunk's B registers makes the end of a chunk wait for
+  // them; an unrolled ping-pong without that wait, and a third register set,
+  // both measured slower.
   if constexpr (kLdsB) {
+    // The block's slices run back to back: during the last chunk of a slice
+    // the first chunk of the next one loads (same A rows, the next columns'
+    // weights), so the next slice starts without the load latency and the
+    // epilogue's stores overlap the loads.
     a_load(0, tail_chunk(0));
     a_store(0);
     __syncthreads();
-    for (uint32_t c = 0; c < chunks; ++c) {
-      const bool more = c + 1 < chunks;
-      if (more) a_load((c + 1) * kCG, tail_chunk(c + 1));
-      compute(0, b0);
-      __syncthreads();
-      if (more) {
-        a_store(0);
+    if constexpr (slices_per_block<EPI>() == 1) {
+      // one slice: the epilogue after the loop, where the loop's offsets are dead
+      for (uint32_t c = 0; c < chunks; ++c) {
+        const bool more = c + 1 < chunks;
+        if (more) a_load((c + 1) * kCG, tail_chunk(c + 1));
+        compute(0, b0);
         __syncthreads();
+        if (more) {
+          a_store(0);
+          __syncthreads();
+        }
+      }
+      epilogue(slice0);
+      return;
+    }
+    for (uint32_t k = 0; k < nslices; ++k) {
+      for (uint32_t c = 0; c < chunks; ++c) {
+        const bool more = c + 1 < chunks || k + 1 < nslices;
+        if (c + 1 < chunks) {
+          a_load((c + 1) * kCG, tail_chunk(c + 1));
+        } else if (more) {
+          next_slice();
+          a_load(0, tail_chunk(0));
+        }
+        compute(0, b0);
+        __syncthreads();
+        if (more) {
+          a_store(0);
+          __syncthreads();
+        }
+        if (c + 1 == chunks) {  // after the store: the prefetch registers are free for the epilogue
+          epilogue(slice);
+#pragma unroll
+          for (int pj = 0; pj < PROJ; ++pj)
+#pragma unroll
+            for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+              for (int mb = 0; mb < MBU; ++mb) acc[pj][nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          ++slice;
+        }
       }
     }
   } else {
@@ -533,33 +627,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       }
       __syncthreads();
     }
-  }
-
-  // epilogue: lane holds rows 4*(lane/16) + i of every row block, column lane%16
-#pragma unroll
-  for (int nb = 0; nb < NBW; ++nb) {
-    const uint32_t col = n_wave + nb * 16 + bn;
-    if (col >= N) continue;
-#pragma unroll
-    for (int mb = 0; mb < MBU; ++mb) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t r = mb * 16 + 4 * bkb + i;
-        if (r >= rows) continue;
-        const size_t o = static_cast<size_t>(row0 + r) * N + col;
-        if constexpr (EPI == kEpiSwiglu) {
-          const float gv = round_bf16(acc[0][nb][mb][i]);
-          const float uv = round_bf16(acc[PROJ - 1][nb][mb][i]);
-          ActBF16::store(p.out, o, swiglu_act<ActBF16>(gv, uv));
-        } else if constexpr (EPI == kEpiRows) {
-          ActBF16::store(p.out, o, round_bf16(acc[0][nb][mb][i]));
-        } else {
-          float v = acc[0][nb][mb][i];
-          if (p.bias != nullptr) v += p.bias[col];
-          static_cast<float*>(p.out)[o] = round_bf16(v);
-        }
-      }
-    }
+    epilogue(slice0);
   }
 }
 
@@ -598,16 +666,18 @@ void k_grouped(GroupedLaunch p) {
   // consecutive blocks of the same XCD and share its L2 copy of the tile's A
   // rows.  Sorted tiles: XCD x takes the x-th eighth of the tiles in order,
   // so the row tiles of one expert also follow each other on one XCD and
-  // share its weights.  The grid is slices * (tile bound rounded up to a
-  // multiple of 8); blocks past the live tile count exit.
+  // share its weights.  A block computes p.spb consecutive slices of its
+  // tile (see grouped_tile).  The grid is slices / spb * (tile bound rounded
+  // up to a multiple of 8); blocks past the live tile count exit.
   const uint32_t slices = (p.n_dim + WAVES * NBW * 16 - 1) / (WAVES * NBW * 16);
+  const uint32_t nslices = p.spb, sgroups = slices / nslices;
   const uint32_t lin = blockIdx.x, r8 = lin >> 3;
-  uint32_t slice = r8 % slices;
-  uint32_t tile = (r8 / slices) * 8 + (lin & 7u);
+  const uint32_t slice0 = (r8 % sgroups) * nslices;
+  uint32_t tile = (r8 / sgroups) * 8 + (lin & 7u);
 #if VM_G_MAP == 1
   if (p.tiles != nullptr) {
     const uint32_t chunk = (*p.tile_count + 7u) / 8u;
-    const uint32_t local = r8 / slices;
+    const uint32_t local = r8 / sgroups;
     if (local >= chunk) return;
     tile = (lin & 7u) * chunk + local;
   }
@@ -644,10 +714,11 @@ void k_grouped(GroupedLaunch p) {
       for (int pj = 0; pj < PROJ; ++pj) source_proj(kind, index, p.pool, &p.stream, p.dense[pj], p.part[pj], N, K, w[pj]);
     }
     if (!ok) {  // an unresolved expert: its rows are zero (status flagged)
-      if (tid == 0 && slice == 0) flag(p.status, 1u);
-      for (uint32_t i = tid; i < rows * WAVES * NBW * 16; i += WAVES * 64) {
-        const uint32_t r = i / (WAVES * NBW * 16);
-        const uint32_t col = slice * WAVES * NBW * 16 + i % (WAVES * NBW * 16);
+      if (tid == 0 && slice0 == 0) flag(p.status, 1u);
+      const uint32_t cols = nslices * WAVES * NBW * 16;
+      for (uint32_t i = tid; i < rows * cols; i += WAVES * 64) {
+        const uint32_t r = i / cols;
+        const uint32_t col = slice0 * WAVES * NBW * 16 + i % cols;
         if (col < N) ActBF16::store(p.out, static_cast<size_t>(row0 + r) * N + col, 0.0f);
       }
       return;
@@ -655,15 +726,15 @@ void k_grouped(GroupedLaunch p) {
   }
   const uint32_t mbu = (rows + 15) / 16;  // block-uniform, 1..kMB
   if constexpr (kMB >= 4) {
-    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4>(p, w, row0, rows, slice, s_a0);
+    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 3) {
-    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3>(p, w, row0, rows, slice, s_a0);
+    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 2) {
-    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2>(p, w, row0, rows, slice, s_a0);
+    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2>(p, w, row0, rows, slice0, nslices, s_a0);
   }
-  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1>(p, w, row0, rows, slice, s_a0);
+  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1>(p, w, row0, rows, slice0, nslices, s_a0);
 }
 
 // ------------------------------------------------------------- row tiles ---
@@ -1220,12 +1291,18 @@ hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max
     attr = true;
   }
   const uint32_t cols = WAVES * NBW * 16;
-  const dim3 grid(((p.n_dim + cols - 1) / cols) * ((max_tiles + 7) / 8 * 8));
+  const uint32_t slices = (p.n_dim + cols - 1) / cols;
+  // slices per block: the one-stage path only, and a divisor of the slices
+  uint32_t spb = lds_weights<EPI, TAIL>() && p.n_dim % cols == 0 ? slices_per_block<EPI>() : 1u;
+  while (slices % spb != 0) spb /= 2;
+  GroupedLaunch q = p;
+  q.spb = spb;
+  const dim3 grid(slices / spb * ((max_tiles + 7) / 8 * 8));
   hipEvent_t start = nullptr, stop = nullptr;
   if (timing_events(family, &start, &stop))
-    hipExtLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, start, stop, 0, p);
+    hipExtLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, start, stop, 0, q);
   else
-    hipLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, p);
+    hipLaunchKernelGGL(kernel, grid, dim3(WAVES * 64), lds, stream, q);
   return hipGetLastError();
 }
 

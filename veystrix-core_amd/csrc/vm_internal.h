@@ -232,6 +232,7 @@ struct GroupedLaunch {
   uint64_t* trace;             // phase trace of the 16-row tile kernels (diagnostics), or null
   uint32_t k_dim, n_dim, experts, a_stride;
   uint32_t a_rows;             // rows of the A matrix: the chunked GEMM addresses it with 32-bit byte offsets
+  uint32_t spb;                // column slices per block (set by launch_grouped)
 };
 
 struct SortLaunch {
