@@ -37,6 +37,8 @@
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "vm_internal.h"
 
 namespace vm {
@@ -792,7 +794,6 @@ __device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item,
   constexpr int kQG = kG / 4;                      // groups per lane quarter (2 KCH)
   constexpr int kUnits = kG * 4;                   // 16-byte A units per row
   constexpr int kRowBytes = kUnits * 16;
-  constexpr int kItems = 16 * kUnits / kThreads;   // A units per thread
   static_assert((16 * kUnits) % kThreads == 0, "whole A units per thread");
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t K = p.k_dim, N = p.n_dim;
@@ -836,25 +837,6 @@ __device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item,
   }
   if (p.trace != nullptr) tr.mark(1);
 
-  // A loads: unit it = j * threads + tid -> (row it / kUnits, unit it % kUnits).
-  // Unconditional (branches here made every load wait for the one before):
-  // rows past the tile reload its last row (their outputs are not stored; an
-  // MFMA output row depends on its own A row only).
-  const bool gather = p.row_token != nullptr;
-  uint4 av[kItems];
-#pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const uint32_t it = j * kThreads + tid;
-    const uint32_t r = min(it / kUnits, rows - 1), u = it % kUnits;
-    uint32_t arow;
-    if constexpr (kUnits % 64 == 0) {  // r is wave-uniform
-      arow = gather ? __builtin_amdgcn_readlane(my_row, __builtin_amdgcn_readfirstlane(r)) : row0 + r;
-    } else {
-      arow = gather ? __shfl(my_row, static_cast<int>(r), 64) : row0 + r;
-    }
-    av[j] = ldg16(p.a + static_cast<size_t>(arow) * p.a_stride + u * 8u);
-  }
-
   // B: lane -> column lane % 16 of the wave's block, quarter q = lane / 16;
   // columns past N read the last row and are not stored
   const uint32_t bn = lane & 15u, q = lane >> 4;
@@ -862,43 +844,76 @@ __device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item,
   const uint32_t col_ld = min(n_col, N - 1);
   const uint32_t g_lane = q * kQG;                 // the lane's first group
   uint32_t sv[PROJ][KCH], bv[PROJ][KCH];           // bf16 pairs of groups g_lane + 2 i, + 2 i + 1
-#pragma unroll
-  for (int pj = 0; pj < PROJ; ++pj) {
-    const size_t m = (static_cast<size_t>(col_ld) * kG + g_lane) * 2u;
-    ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].s) + m, sv[pj]);
-    ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].b) + m, bv[pj]);
-  }
   const uint8_t* wl[PROJ];
 #pragma unroll
   for (int pj = 0; pj < PROJ; ++pj)
     wl[pj] = reinterpret_cast<const uint8_t*>(w[pj].w) + (static_cast<size_t>(col_ld) * kG + g_lane) * 16u;
   constexpr int kDepth = KCH < kRowsDepth ? KCH : kRowsDepth;
   uint4 bw[kDepth][PROJ][2];
-  // keep the prefetch here and in chunk order: the scheduler otherwise sinks
-  // every chunk's loads to just before their first use, or mixes the chunks,
-  // and each chunk then waits for all outstanding loads
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int d = 0; d < kDepth; ++d) {
+  // the lane's scales and biases, then the first kDepth chunks of weights
+  auto b_issue = [&]() {
 #pragma unroll
     for (int pj = 0; pj < PROJ; ++pj) {
-      bw[d][pj][0] = ldg16(wl[pj] + d * 32u);
-      bw[d][pj][1] = ldg16(wl[pj] + d * 32u + 16u);
+      const size_t m = (static_cast<size_t>(col_ld) * kG + g_lane) * 2u;
+      ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].s) + m, sv[pj]);
+      ldg_dwords<KCH>(reinterpret_cast<const uint8_t*>(w[pj].b) + m, bv[pj]);
     }
+    // keep the prefetch here and in chunk order: the scheduler otherwise sinks
+    // every chunk's loads to just before their first use, or mixes the chunks,
+    // and each chunk then waits for all outstanding loads
     __builtin_amdgcn_sched_barrier(0);
-  }
-
-  if (p.trace != nullptr) tr.mark(2);
 #pragma unroll
-  for (int j = 0; j < kItems; ++j) {
-    const uint32_t it = j * kThreads + tid;
-    const uint32_t r = it / kUnits, u = it % kUnits;
-    const uint4 x = av[j];
-    const uint4 pp = make_uint4((x.x & 0xffffu) | (x.z << 16), (x.x >> 16) | (x.z & 0xffff0000u),
-                                (x.y & 0xffffu) | (x.w << 16), (x.y >> 16) | (x.w & 0xffff0000u));
-    const uint32_t phys = (u & ~15u) | ((u ^ rows_swz(r, u / (kQG * 4))) & 15u);
-    *reinterpret_cast<uint4*>(s_a + r * kRowBytes + phys * 16u) = pp;
-  }
+    for (int d = 0; d < kDepth; ++d) {
+#pragma unroll
+      for (int pj = 0; pj < PROJ; ++pj) {
+        bw[d][pj][0] = ldg16(wl[pj] + d * 32u);
+        bw[d][pj][1] = ldg16(wl[pj] + d * 32u + 16u);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // A rows: R rows of the tile are loaded (R = 4, 8 or 16, the least that
+  // holds it and gives every thread whole units); LDS rows past R keep stale
+  // data, which only reaches MFMA output rows that are not stored (an output
+  // row depends on its own A row only).  Unit it = j * threads + tid -> (row
+  // it / kUnits, unit it % kUnits).  The loads are unconditional (branches
+  // here made every load wait for the one before): rows past the tile reload
+  // its last row.
+  const bool gather = p.row_token != nullptr;
+  auto stage = [&](auto rows_class) {
+    constexpr int R = decltype(rows_class)::value;
+    constexpr int kIt = R * kUnits / kThreads;
+    uint4 av[kIt];
+#pragma unroll
+    for (int j = 0; j < kIt; ++j) {
+      const uint32_t it = j * kThreads + tid;
+      const uint32_t r = min(it / kUnits, rows - 1), u = it % kUnits;
+      uint32_t arow;
+      if constexpr (kUnits % 64 == 0) {  // r is wave-uniform
+        arow = gather ? __builtin_amdgcn_readlane(my_row, __builtin_amdgcn_readfirstlane(r)) : row0 + r;
+      } else {
+        arow = gather ? __shfl(my_row, static_cast<int>(r), 64) : row0 + r;
+      }
+      av[j] = ldg16(p.a + static_cast<size_t>(arow) * p.a_stride + u * 8u);
+    }
+    b_issue();
+    if (p.trace != nullptr) tr.mark(2);
+#pragma unroll
+    for (int j = 0; j < kIt; ++j) {
+      const uint32_t it = j * kThreads + tid;
+      const uint32_t r = it / kUnits, u = it % kUnits;
+      const uint4 x = av[j];
+      const uint4 pp = make_uint4((x.x & 0xffffu) | (x.z << 16), (x.x >> 16) | (x.z & 0xffff0000u),
+                                  (x.y & 0xffffu) | (x.w << 16), (x.y >> 16) | (x.w & 0xffff0000u));
+      const uint32_t phys = (u & ~15u) | ((u ^ rows_swz(r, u / (kQG * 4))) & 15u);
+      *reinterpret_cast<uint4*>(s_a + r * kRowBytes + phys * 16u) = pp;
+    }
+  };
+  constexpr bool kR4 = (4 * kUnits) % kThreads == 0, kR8 = (8 * kUnits) % kThreads == 0;
+  if (kR4 && rows <= 4) stage(std::integral_constant<int, kR4 ? 4 : 16>{});
+  else if (kR8 && rows <= 8) stage(std::integral_constant<int, kR8 ? 8 : 16>{});
+  else stage(std::integral_constant<int, 16>{});
   __syncthreads();
   if (p.trace != nullptr) tr.mark(3);
 
