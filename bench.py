@@ -814,9 +814,9 @@ def main():
         log("batched decode at the distinct-expert count of i.i.d. Zipf(1.1) draws (~133)")
         result["batched_133_distinct"] = run_grouped("batched", 32, 8, 50, args.seed, target_distinct=133)
         log("chunked prefill: 2048 rows")
-        result["prefill"] = run_grouped("prefill", 2048, 3, 8, args.seed)
+        result["prefill"] = run_grouped("prefill", 2048, 8, 20, args.seed)
         log("layer-major prefill window: four 2048-row chunks per layer call")
-        result["prefill_window"] = run_grouped("prefill", 8192, 3, 4, args.seed)
+        result["prefill_window"] = run_grouped("prefill", 8192, 4, 10, args.seed)
         result["prefill_window"]["window"] = "4 chunks x 2048 rows in one layer call (layer-major order)"
     if not args.no_stack:
         log("48-layer stack, LRU pool of 6 GB, misses from pinned host")

@@ -1091,6 +1091,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.n_dim = g.I;
   q.a_stride = g.H;
   q.a_rows = g.T;
+  // routed rows per expert on average: at most one row tile each
+  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * vm::kGroupedRows;
   e = w.small ? vm::launch_rows(vm::kEpiSwiglu, q, w.max_tiles, stream)
               : vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped gate/up launch");
@@ -1107,6 +1109,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.n_dim = g.H;
   q.a_stride = g.I;
   q.a_rows = g.T * g.K + (g.shared ? g.T : 0);
+  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * vm::kGroupedRowsDown;
   q.tiles = s.tiles_dn;
   q.tile_count = s.tile_count_dn;
   e = w.small ? vm::launch_rows(vm::kEpiRows, q, w.max_tiles_dn, stream)

@@ -283,7 +283,7 @@ constexpr uint32_t slices_per_block() {
 // staging covers those rows only and the MFMA loops carry no branch, so the
 // LDS reads of a step and the MFMAs of neighbouring steps can be scheduled
 // freely.
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU, bool WNT>
 __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjPtrs (&w)[PROJ], uint32_t row0,
                                              uint32_t rows, uint32_t slice0, uint32_t nslices, uint8_t* s_a0) {
   constexpr bool Q4 = EPI != kEpiLogits;
@@ -407,7 +407,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
     for (int j = 0; j < kWItems; ++j) {
       constexpr int kPerProj = kCols * kCG;
       const int pj = (j * kThreads) / kPerProj;  // compile-time
-      wr[j] = ldg16(reinterpret_cast<const uint8_t*>(w[pj].w) + g0 * 16u + opaque(w_vo[j]));
+      const uint8_t* src = reinterpret_cast<const uint8_t*>(w[pj].w) + g0 * 16u + opaque(w_vo[j]);
+      wr[j] = WNT ? ldg16_nt(src) : ldg16(src);
     }
   };
   // (x0 x1)(x2 x3)(x4 x5)(x6 x7) -> (x0 x4)(x1 x5)(x2 x6)(x3 x7)
@@ -651,7 +652,13 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #ifndef VM_G_MAP
 #define VM_G_MAP 1
 #endif
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+// WNT: the weight lines are loaded non-temporal, for calls whose experts
+// mostly hold one row tile (each line is read once; kept from the L2 they
+// displaced the tile's activation rows, which the column slices share: the
+// 2048-row gate/up fetched 28 % above its bytes).  Calls with several row
+// tiles per expert keep cached loads (the tiles of an expert share its
+// weights in the L2; non-temporal loads there cost 5 %).
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(EPI == kEpiRows ? VM_DN_WAVES_PER_EU : VM_G_WAVES_PER_EU)))
 void k_grouped(GroupedLaunch p) {
@@ -728,15 +735,15 @@ void k_grouped(GroupedLaunch p) {
   }
   const uint32_t mbu = (rows + 15) / 16;  // block-uniform, 1..kMB
   if constexpr (kMB >= 4) {
-    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 3) {
-    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 2) {
-    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
   }
-  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1>(p, w, row0, rows, slice0, nslices, s_a0);
+  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
 }
 
 // ------------------------------------------------------------- row tiles ---
@@ -1293,11 +1300,11 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
   return hipGetLastError();
 }
 
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
 hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
   // one LDS stage with staged weights (see grouped_tile), else two
   constexpr uint32_t lds = (lds_weights<EPI, TAIL>() ? 1 : 2) * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
-  auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL>;
+  auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL, WNT>;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -1323,8 +1330,11 @@ hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max
 
 template <int EPI, int WAVES, int NBW, int PROJ>
 hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
-  if ((p.k_dim / kGroup) % kCG != 0) return grouped_go_k<EPI, WAVES, NBW, PROJ, true>(family, p, max_tiles, stream);
-  return grouped_go_k<EPI, WAVES, NBW, PROJ, false>(family, p, max_tiles, stream);
+  if ((p.k_dim / kGroup) % kCG != 0)
+    return grouped_go_k<EPI, WAVES, NBW, PROJ, true, false>(family, p, max_tiles, stream);
+  if (lds_weights<EPI, false>() && p.weights_once)
+    return grouped_go_k<EPI, WAVES, NBW, PROJ, false, lds_weights<EPI, false>()>(family, p, max_tiles, stream);
+  return grouped_go_k<EPI, WAVES, NBW, PROJ, false, false>(family, p, max_tiles, stream);
 }
 
 }  // namespace

@@ -74,6 +74,13 @@ __device__ __forceinline__ uint4 ldg16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// A streaming load (non-temporal): data read once, kept from displacing
+// reused lines in the L2.
+__device__ __forceinline__ uint4 ldg16_nt(const void* p) {
+  const vm_u32x4 v = __builtin_nontemporal_load((const __attribute__((address_space(1))) vm_u32x4*)(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ uint32_t ldg_u16(const void* p) {
   return *(const __attribute__((address_space(1))) unsigned short*)(p);
 }

@@ -233,6 +233,7 @@ struct GroupedLaunch {
   uint32_t k_dim, n_dim, experts, a_stride;
   uint32_t a_rows;             // rows of the A matrix: the chunked GEMM addresses it with 32-bit byte offsets
   uint32_t spb;                // column slices per block (set by launch_grouped)
+  bool weights_once;           // most groups hold one row tile: stream the weights past the L2
 };
 
 struct SortLaunch {
