@@ -563,8 +563,10 @@ static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint
   w.tile_count = take(4);
   w.tiles_dn = take(uint64_t(w.max_tiles_dn) * 8);
   w.tile_count_dn = take(4);
-  w.sort_counts = take(1024 * 4);
-  w.sort_cursors = take(1024 * 4);
+  // the counts and the cursors of the multi-block sort, one region (the
+  // router GEMM zeroes both in one pass when the select counts the rows)
+  w.sort_counts = take(2048 * 4);
+  w.sort_cursors = w.sort_counts + 1024 * 4;
   w.row_token = take(uint64_t(w.rows_total) * 4);
   w.pair_row = take(uint64_t(T) * K * 4);
   w.act = take(uint64_t(w.rows_total) * I * 2);
@@ -1037,6 +1039,7 @@ struct GroupedExperts {
   uint32_t* status;
   uint32_t T, K, H, I, E;
   int mode;
+  bool counted;  // the sort's counters were zeroed by the router GEMM
 };
 
 static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char* ws, hipStream_t stream) {
@@ -1064,7 +1067,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   s.shared_rows = g.shared ? g.T : 0;
   s.tile_rows = w.tile_rows;
   s.tile_rows_dn = w.tile_rows_dn;
-  hipError_t e = vm::launch_sort(s, stream);
+  hipError_t e = g.counted ? vm::launch_sort_counted(s, stream) : vm::launch_sort(s, stream);
   if (e != hipSuccess) return hip_fail(e, "sort launch");
 
   vm::GroupedLaunch q{};
@@ -1191,6 +1194,11 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   uint16_t* sig = reinterpret_cast<uint16_t*>(ws + w.sig);
   const uint32_t phases = a->phases == 0 ? (VM_PHASE_ROUTER | VM_PHASE_EXPERTS) : a->phases;
   hipError_t e = hipSuccess;
+  // Calls above the one-block sort's size that run the router GEMM and the
+  // experts together: the GEMM zeroes the sort's counters, so the sort is a
+  // count and one layout + scatter launch.
+  const bool counted = T > kFrontMaxTokens && uint64_t(T) * K > vm::kSortOneBlockPairs &&
+                       (phases & VM_PHASE_ROUTER) && (phases & VM_PHASE_EXPERTS);
   // Calls that take the router GEMM run the shared expert on the side stream,
   // into the last T rows of the activation and expert-row buffers (the routed
   // rows take at most the first T * K).
@@ -1246,6 +1254,10 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     r.a_stride = H;
     r.a_rows = T;
     r.experts = E;
+    if (counted) {
+      r.zero_words = reinterpret_cast<uint32_t*>(ws + w.sort_counts);
+      r.zero_count = 2048;
+    }
     e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
     if (e != hipSuccess) return done(hip_fail(e, "router launch"));
     if (shared && side == nullptr) {
@@ -1296,6 +1308,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   g.I = I;
   g.E = E;
   g.mode = 1;  // rows > 8: the reference's generic combine
+  g.counted = counted;
   return done(run_grouped_experts(g, w, ws, stream));
 }
 

@@ -634,6 +634,9 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   }
 }
 
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+__device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t lin, uint8_t* s_a0);
+
 // EPI: 0 SwiGLU of projections 0 (gate) and 1 (up) -> bf16 [rows, N];
 //      1 bf16 rows -> [rows, N]; 2 router logits (bf16 weights) -> fp32 [rows, N].
 // TAIL: K is not a multiple of the chunk (kCG groups); the last chunk clamps.
@@ -662,10 +665,7 @@ template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(EPI == kEpiRows ? VM_DN_WAVES_PER_EU : VM_G_WAVES_PER_EU)))
 void k_grouped(GroupedLaunch p) {
-  constexpr int kBM = tile_rows<EPI>();
-  constexpr int kMB = kBM / 16;  // MFMA row blocks
-  static_assert(kBM % 16 == 0 && kBM <= 64, "tiles are one to four 16-row blocks");
-  constexpr bool Q4 = EPI != kEpiLogits;
+  static_assert(tile_rows<EPI>() % 16 == 0 && tile_rows<EPI>() <= 64, "tiles are one to four 16-row blocks");
   extern __shared__ uint4 s_dyn[];  // two stages of stage_bytes<...>()
   uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
   const uint32_t tid = threadIdx.x;
@@ -678,9 +678,23 @@ void k_grouped(GroupedLaunch p) {
   // share its weights.  A block computes p.spb consecutive slices of its
   // tile (see grouped_tile).  The grid is slices / spb * (tile bound rounded
   // up to a multiple of 8); blocks past the live tile count exit.
+  if constexpr (EPI == kEpiLogits) {
+    if (blockIdx.x == 0 && p.zero_words != nullptr)
+      for (uint32_t i = tid; i < p.zero_count; i += WAVES * 64) p.zero_words[i] = 0;
+  }
+  grouped_block<EPI, WAVES, NBW, PROJ, TAIL, WNT>(p, blockIdx.x, s_a0);
+}
+
+// One block's work item `lin` (the XCD-aware order of k_grouped).
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+__device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t lin, uint8_t* s_a0) {
+  constexpr int kBM = tile_rows<EPI>();
+  constexpr int kMB = kBM / 16;  // MFMA row blocks
+  constexpr bool Q4 = EPI != kEpiLogits;
+  const uint32_t tid = threadIdx.x;
   const uint32_t slices = (p.n_dim + WAVES * NBW * 16 - 1) / (WAVES * NBW * 16);
   const uint32_t nslices = p.spb, sgroups = slices / nslices;
-  const uint32_t lin = blockIdx.x, r8 = lin >> 3;
+  const uint32_t r8 = lin >> 3;
   const uint32_t slice0 = (r8 % sgroups) * nslices;
   uint32_t tile = (r8 / sgroups) * 8 + (lin & 7u);
 #if VM_G_MAP == 1
@@ -1020,7 +1034,7 @@ __device__ uint32_t block_scan_1024(uint32_t v, uint32_t* s_wave) {
 // Row offsets, both tile lists (group, first row) of the gate/up and the down
 // tiles, from the row count n of group g = threadIdx.x (one block of 1024
 // threads).  Returns the group's first row.
-__device__ uint32_t sort_layout(const SortLaunch& p, uint32_t n, uint32_t* s_wave) {
+__device__ uint32_t sort_layout(const SortLaunch& p, uint32_t n, uint32_t* s_wave, bool write = true) {
   const uint32_t g = threadIdx.x;
   const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
   const uint32_t nt = (n + p.tile_rows - 1) / p.tile_rows;
@@ -1029,6 +1043,7 @@ __device__ uint32_t sort_layout(const SortLaunch& p, uint32_t n, uint32_t* s_wav
   const uint32_t tile_end = block_scan_1024(nt, s_wave);
   const uint32_t tile_end_dn = block_scan_1024(nt_dn, s_wave);
   const uint32_t row_begin = row_end - n, tile_begin = tile_end - nt, tile_begin_dn = tile_end_dn - nt_dn;
+  if (!write) return row_begin;
   if (g < groups) {
     p.row_off[g] = row_begin;
     for (uint32_t i = 0; i < nt; ++i) p.tiles[tile_begin + i] = make_uint2(g, i * p.tile_rows);
@@ -1162,6 +1177,60 @@ __global__ __launch_bounds__(kSortThreads) void k_sort_scatter(SortLaunch p) {
       p.pair_row[i] = kNoRow;
     }
   }
+}
+
+// The layout and scatter of the sort when k_sort_count has filled p.counts
+// and p.cursors was zeroed before it: one launch.  Every block lays the rows
+// out from the counts (the same scans; block 0 writes the row offsets, tile
+// lists and the shared rows' tokens), counts its own pairs in LDS, reserves
+// each expert's run of rows with one atomic on the zeroed cursor and scatters
+// its pairs into it.
+constexpr uint32_t kPlacePerThread = 2;
+constexpr uint32_t kPlaceBlockPairs = 1024 * kPlacePerThread;
+
+__global__ __launch_bounds__(1024) void k_sort_place(SortLaunch p) {
+  __shared__ uint32_t s_wave[16];
+  __shared__ uint32_t s_count[1024];
+  __shared__ uint32_t s_base[1024];
+  __shared__ uint32_t s_shared_first;
+  const uint32_t g = threadIdx.x;
+  const uint32_t pairs = p.tokens * p.slots;
+  const uint32_t groups = p.experts + (p.shared_rows != 0 ? 1u : 0u);
+  const uint32_t base = blockIdx.x * kPlaceBlockPairs;
+  uint32_t e[kPlacePerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kPlacePerThread; ++j)
+    e[j] = static_cast<uint32_t>(p.inds[min(base + j * 1024 + g, pairs - 1)]);
+  uint32_t n = 0;
+  if (g < p.experts) n = p.counts[g];
+  else if (g < groups) n = p.shared_rows;
+  s_count[g] = 0;
+  const uint32_t row_begin = sort_layout(p, n, s_wave, blockIdx.x == 0);
+  if (g == p.experts) s_shared_first = row_begin;
+  uint32_t local[kPlacePerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kPlacePerThread; ++j) {
+    local[j] = 0;
+    if (base + j * 1024 + g < pairs && e[j] < p.experts) local[j] = atomicAdd(&s_count[e[j]], 1u);
+  }
+  __syncthreads();
+  if (g < p.experts && s_count[g] != 0) s_base[g] = row_begin + atomicAdd(&p.cursors[g], s_count[g]);
+  __syncthreads();
+#pragma unroll
+  for (uint32_t j = 0; j < kPlacePerThread; ++j) {
+    const uint32_t i = base + j * 1024 + g;
+    if (i >= pairs) continue;
+    if (e[j] < p.experts) {
+      const uint32_t pos = s_base[e[j]] + local[j];
+      p.row_token[pos] = i / p.slots;
+      p.pair_row[i] = pos;
+    } else {
+      p.pair_row[i] = kNoRow;
+      flag(p.status, 2u);
+    }
+  }
+  if (blockIdx.x == 0)
+    for (uint32_t i = g; i < p.shared_rows; i += 1024) p.row_token[s_shared_first + i] = i;
 }
 
 // --------------------------------------------------------------- combine ---
@@ -1429,8 +1498,6 @@ hipError_t launch_rows(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipS
   return hipErrorInvalidValue;
 }
 
-// Calls up to this many (token, slot) pairs sort in one block.
-constexpr uint32_t kSortOneBlockPairs = 4096;
 
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
   const uint32_t pairs = p.tokens * p.slots;
@@ -1440,6 +1507,15 @@ hipError_t launch_sort(const SortLaunch& p, hipStream_t stream) {
   if (e == hipSuccess) e = launch("sort", k_sort_count, blocks, dim3(kSortThreads), stream, p);
   if (e == hipSuccess) e = launch("sort", k_sort_scan, dim3(1), dim3(1024), stream, p);
   if (e == hipSuccess) e = launch("sort", k_sort_scatter, blocks, dim3(kSortThreads), stream, p);
+  return e;
+}
+
+hipError_t launch_sort_counted(const SortLaunch& p, hipStream_t stream) {
+  const uint32_t pairs = p.tokens * p.slots;
+  hipError_t e = launch("sort", k_sort_count, dim3((pairs + kSortBlockPairs - 1) / kSortBlockPairs),
+                        dim3(kSortThreads), stream, p);
+  if (e == hipSuccess)
+    e = launch("sort", k_sort_place, dim3((pairs + kPlaceBlockPairs - 1) / kPlaceBlockPairs), dim3(1024), stream, p);
   return e;
 }
 

@@ -234,6 +234,10 @@ struct GroupedLaunch {
   uint32_t a_rows;             // rows of the A matrix: the chunked GEMM addresses it with 32-bit byte offsets
   uint32_t spb;                // column slices per block (set by launch_grouped)
   bool weights_once;           // most groups hold one row tile: stream the weights past the L2
+  // router GEMM only: block 0 zeroes zero_count words at zero_words (the
+  // counters of the sort that follows the select)
+  uint32_t* zero_words;
+  uint32_t zero_count;
 };
 
 struct SortLaunch {
@@ -275,7 +279,13 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
 constexpr int kRowsTile = 16;
 bool rows_supported(uint32_t k_dim);
 hipError_t launch_rows(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
+// Calls up to this many (token, slot) pairs sort in one block.
+constexpr uint32_t kSortOneBlockPairs = 4096;
 hipError_t launch_sort(const SortLaunch& p, hipStream_t stream);
+// The sort when p.counts and p.cursors were zeroed before it (by the router
+// GEMM): per-block histograms into the counts, then one launch lays out the
+// rows and tiles and scatters the pairs.
+hipError_t launch_sort_counted(const SortLaunch& p, hipStream_t stream);
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream);
 hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
                               uint32_t hidden, hipStream_t stream);
