@@ -277,7 +277,11 @@ def run_grouped(name, tokens, layers, reps, seed, target_distinct=None):
     torch.cuda.synchronize()
     lib.vm_timing_enable(0)
     kernels = {}
-    for fam in ("router", "router_gemm", "select", "sort", "grouped_gateup", "grouped_down", "combine"):
+    # shared_*: the shared expert of calls above 64 rows, on a side stream
+    # beside the router GEMM, selection and sort (its durations include that
+    # sharing of the CUs)
+    for fam in ("router", "router_gemm", "select", "sort", "grouped_gateup", "grouped_down", "combine",
+                "shared_gate", "shared_gateup", "shared_down"):
         total, launches = ctypes.c_double(), ctypes.c_uint64()
         _lib.check(lib.vm_timing_read(fam.encode(), ctypes.byref(total), ctypes.byref(launches)))
         if launches.value:

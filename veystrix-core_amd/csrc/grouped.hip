@@ -1432,10 +1432,16 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
   if (p.a_rows == 0 || static_cast<uint64_t>(p.a_rows) * p.a_stride * 2u > 0xffffffffull ||
       static_cast<uint64_t>(p.n_dim) * p.k_dim > 0xffffffffull)
     return hipErrorInvalidValue;
+  // a call with no routed experts is the shared expert's own GEMM (run on a
+  // side stream beside the routing), timed apart from the routed experts
+  const bool own = p.experts == 0;
   switch (epi) {
     case kEpiSwiglu:
-      return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>("grouped_gateup", p, max_tiles, stream);
-    case kEpiRows: return grouped_go<kEpiRows, VM_DN_WAVES, VM_DN_NBW, 1>("grouped_down", p, max_tiles, stream);
+      return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>(own ? "shared_gateup" : "grouped_gateup", p,
+                                                               max_tiles, stream);
+    case kEpiRows:
+      return grouped_go<kEpiRows, VM_DN_WAVES, VM_DN_NBW, 1>(own ? "shared_down" : "grouped_down", p, max_tiles,
+                                                             stream);
     default: return grouped_go<kEpiLogits, 4, 1, 1>("router_gemm", p, max_tiles, stream);
   }
 }
@@ -1527,7 +1533,7 @@ hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {
 
 hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
                               uint32_t hidden, hipStream_t stream) {
-  return launch("router", k_shared_gate, dim3(tokens), dim3(64), stream, x, seg, sig, hidden);
+  return launch("shared_gate", k_shared_gate, dim3(tokens), dim3(64), stream, x, seg, sig, hidden);
 }
 
 }  // namespace vm
