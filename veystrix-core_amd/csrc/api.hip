@@ -535,6 +535,11 @@ constexpr uint32_t kRowsMaxTokens = 64;
 #ifndef VM_ROWS_PATH
 #define VM_ROWS_PATH 1
 #endif
+// Router logits of calls above 64 rows: the LDS-ring bf16 GEMM (1) or the
+// chunked GEMM shared with the Q4 projections (0).
+#ifndef VM_ROUTER_RING
+#define VM_ROUTER_RING 1
+#endif
 static bool small_grouped(uint32_t T, uint32_t H, uint32_t I) {
   return VM_ROWS_PATH && T <= kRowsMaxTokens && vm::rows_supported(H) && vm::rows_supported(I);
 }
@@ -1258,7 +1263,9 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
       r.zero_words = reinterpret_cast<uint32_t*>(ws + w.sort_counts);
       r.zero_count = 2048;
     }
-    e = vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
+    e = VM_ROUTER_RING && vm::router_gemm_supported(H, E)
+            ? vm::launch_router_gemm(r, stream)
+            : vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
     if (e != hipSuccess) return done(hip_fail(e, "router launch"));
     if (shared && side == nullptr) {
       e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T, H,

@@ -240,6 +240,13 @@ struct GroupedLaunch {
   uint32_t zero_count;
 };
 
+// Router logits of grouped calls as a bf16 GEMM streamed through an LDS ring
+// (router_gemm.hip): fp32 [rows, n_dim] = round_bf16(a . bf16_weight^T +
+// bias), block 0 zeroing zero_words.  Shapes: k_dim 1024, 2048 or 4096,
+// n_dim a multiple of 64, a_stride == k_dim.
+bool router_gemm_supported(uint32_t k_dim, uint32_t n_dim);
+hipError_t launch_router_gemm(const GroupedLaunch& p, hipStream_t stream);
+
 struct SortLaunch {
   const int32_t* inds;         // [tokens, slots]
   uint32_t* row_off;           // [groups + 1]
