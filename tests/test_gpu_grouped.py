@@ -105,6 +105,44 @@ def test_grouped_layer_many_rows_per_expert(device):
     _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, "grouped layer T=2048 (sample)")
 
 
+@pytest.mark.parametrize("hidden,experts,tokens", [(4096, 128, 300), (4096, 128, 8256), (1024, 512, 4096)],
+                         ids=["k4096-8stage", "k4096-4stage", "k1024-4stage"])
+def test_router_gemm_instances(device, hidden, experts, tokens):
+    """The router GEMM of calls above 64 rows at the K and ring depths the
+    prefill shapes do not reach (K = 4096 with eight and four stages, K = 1024
+    with four): the experts chosen per row equal the decode router's, which
+    sums every logit in another order, except on near ties (bounded, and
+    checked against the oracle's gates); at 300 rows the whole layer is
+    compared with the oracle."""
+    from veymoe.router import router_topk
+
+    spec = synth.LayerSpec(f"router_k{hidden}", hidden, 256, experts, 6, 0, tokens)
+    seed = 340 + hidden // 1024 + experts
+    layer = assemble.build_layer(spec, seed, device, dense=True)
+    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
+    x = bf16_device(x_np, device)
+    y = layer(x)
+    grouped = layer.last_inds.sort(dim=1).values
+    decode, _ = router_topk(x, layer.gate.weight, spec.top_k)
+    decode = decode.sort(dim=1).values
+    torch.cuda.synchronize()
+    differ = np.nonzero(~(grouped == decode).all(dim=1).cpu().numpy())[0]
+    print(f"[selection] router GEMM K={hidden} E={experts} T={tokens}: {len(differ)} rows differ from the "
+          f"decode router", flush=True)
+    if len(differ):
+        layer_np = synth.numpy_layer(spec, seed)
+        _, _, gates = mo.route(x_np[differ], layer_np["router"], spec.top_k, "bf16", layer_np.get("router_bias"))
+        for i in range(len(differ)):
+            assert _near_tie(gates[i], spec.top_k), int(differ[i])
+    assert len(differ) <= max(1, tokens // 1000)
+    if tokens <= 512:
+        rows = np.arange(tokens)
+        ref = _layer_ref(spec, seed, x_np, rows)
+        same = _check_selection(layer.last_inds.cpu().numpy(), ref, spec.top_k, max(1, tokens // 20),
+                                f"K={hidden} T={tokens}")
+        _assert_layer(host(y), spec, seed, x_np, rows, same, ref, f"layer K={hidden} T={tokens}")
+
+
 def test_grouped_batched_config_pool(device):
     """The full-size layer with Zipf(1.1) routing at 32 tokens, experts in a
     pool behind a permuted slot table, shared expert included."""
