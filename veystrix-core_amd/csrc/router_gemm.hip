@@ -8,11 +8,14 @@
 // ring of S stages of 64 K-inputs each, so S - 1 stages are in flight while
 // one is multiplied.
 //
-//   tile     64 rows x 64 columns per 4-wave block; wave (wm, wn) owns rows
-//            32 wm .. +32 and columns 32 wn .. +32 (two 16-row by two
-//            16-column MFMA blocks), so a K step reads two A and two B
-//            fragments for four v_mfma_f32_16x16x32_bf16.
-//   stage    A rows then W rows, 128 bytes (64 inputs) each: 8 KB + 8 KB.
+//   tile     64 TM rows x 64 TM columns per 4-wave block (TM = 1 or 2);
+//            wave (wm, wn) owns rows 32 TM wm .. +32 TM and as many columns
+//            from 32 TM wn (2 TM by 2 TM MFMA blocks of 16 x 16), so a K step
+//            reads 2 TM A and 2 TM B fragments for 4 TM^2
+//            v_mfma_f32_16x16x32_bf16.  TM = 2 halves the rows and router
+//            rows that reach LDS per logit (each is read once per tile of the
+//            other operand); it is used while it still gives every CU a block.
+//   stage    A rows then W rows, 128 bytes (64 inputs) each: TM (8 KB + 8 KB).
 //            The 16-byte unit u of row r sits at unit u ^ swz(r), swz(r)
 //            moving row bits 2 and 1 onto unit bits 1 and 2.  An MFMA read
 //            (lane l: row l % 16, unit 4 ks + l / 16) then lands on the bank
@@ -40,6 +43,7 @@
 #include <hip/hip_runtime.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "vm_internal.h"
 
@@ -50,22 +54,31 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int kRtRows = 64;        // tile rows
-constexpr int kRtCols = 64;        // tile columns
 constexpr int kRtK = 64;           // K inputs per stage
 constexpr int kRtRowBytes = kRtK * 2;
-constexpr int kRtHalf = kRtRows * kRtRowBytes;  // bytes of the A (or W) rows of a stage
 constexpr int kRtThreads = 256;
-constexpr int kRtDmaPerWave = 2 * kRtHalf / 1024 / (kRtThreads / 64);  // 1 KB DMA loads per wave and stage
-static_assert(kRtRows == kRtCols, "the A and W halves of a stage share one layout");
-static_assert(kRtDmaPerWave == 4, "four DMA loads per wave and stage");
+// Tile of TM x 64 rows by TM x 64 columns (TM = 1 or 2); a stage holds its A
+// rows then its router rows, 128 bytes each: TM x 16 KB.
+template <int TM>
+constexpr int rt_tile() {
+  return 64 * TM;
+}
+template <int TM>
+constexpr int rt_half() {
+  return rt_tile<TM>() * kRtRowBytes;
+}
+template <int TM>
+constexpr int rt_dma_per_wave() {  // 1 KB DMA loads per wave and stage
+  return 2 * rt_half<TM>() / 1024 / (kRtThreads / 64);
+}
+static_assert(rt_dma_per_wave<1>() == 4 && rt_dma_per_wave<2>() == 8, "whole 1 KB loads per wave");
 
 __device__ __forceinline__ uint32_t rt_swz(uint32_t r) { return ((r >> 1) & 2u) | ((r << 1) & 4u); }
 
 // Stage J of the ring: one LDS object per stage.
-template <int J>
+template <int J, int TM>
 __device__ __forceinline__ uint8_t* rt_stage() {
-  __shared__ uint4 buf[2 * kRtHalf / 16];
+  __shared__ uint4 buf[2 * rt_half<TM>() / 16];
   return reinterpret_cast<uint8_t*>(buf);
 }
 
@@ -95,12 +108,15 @@ __device__ __forceinline__ void rt_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <int S, int NST>
+template <int S, int NST, int TM>
 __global__ __launch_bounds__(kRtThreads) void k_router_gemm(GroupedLaunch p) {
+  constexpr int kTile = rt_tile<TM>(), kHalf = rt_half<TM>(), kDma = rt_dma_per_wave<TM>();
+  constexpr int kB = 2 * TM;  // 16-row (and 16-column) MFMA blocks per wave
+  constexpr uint32_t kAGroups = kTile / 8;  // 1 KB loads of the A rows per stage
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t T = p.rows, K = p.k_dim, E = p.n_dim;
-  const uint32_t slices = E / kRtCols;
-  const uint32_t row_tiles = (T + kRtRows - 1) / kRtRows;
+  const uint32_t slices = E / kTile;
+  const uint32_t row_tiles = (T + kTile - 1) / kTile;
   const uint32_t lin = blockIdx.x, local = lin >> 3;
   const uint32_t tile = (local / slices) * 8u + (lin & 7u), slice = local % slices;
   if (blockIdx.x == 0 && p.zero_words != nullptr) {
@@ -108,32 +124,34 @@ __global__ __launch_bounds__(kRtThreads) void k_router_gemm(GroupedLaunch p) {
     wait_vm<0>();  // the stores leave the vector memory count before the DMA loads are counted
   }
   if (tile >= row_tiles) return;
-  const uint32_t row0 = tile * kRtRows, col0 = slice * kRtCols;
+  const uint32_t row0 = tile * kTile, col0 = slice * kTile;
 
-  // DMA loads: load i of this wave is 1 KB number g = 4 wave + i of the stage
-  // (A rows 8 g .. +8 for g < 8, else W rows 8 (g - 8) .. +8); lane j loads
-  // unit (j % 8) ^ swz(row) of row 8 (g % 8) + j / 8 into bytes 16 j.
-  uint32_t g_off[kRtDmaPerWave];  // byte offsets from the matrix at K input 0
+  // DMA loads: load i of this wave is 1 KB number g = kDma wave + i of the
+  // stage (A rows 8 g .. +8 for g < kAGroups, else router rows 8 (g -
+  // kAGroups) .. +8); lane j loads unit (j % 8) ^ swz(row) of that row
+  // group's row j / 8 into bytes 16 j.
+  uint32_t g_off[kDma];  // byte offsets from the matrix at K input 0
 #pragma unroll
-  for (int i = 0; i < kRtDmaPerWave; ++i) {
-    const uint32_t g = wave * kRtDmaPerWave + i;
-    const uint32_t r = 8u * (g % 8u) + lane / 8u;
+  for (int i = 0; i < kDma; ++i) {
+    const uint32_t g = wave * kDma + i;
+    const uint32_t r = 8u * (g % kAGroups) + lane / 8u;
     const uint32_t u = (lane % 8u) ^ rt_swz(r);
-    const uint32_t src = g < 8u ? min(row0 + r, T - 1u) : col0 + r;
+    const uint32_t src = g < kAGroups ? min(row0 + r, T - 1u) : col0 + r;
     g_off[i] = (src * K + u * 8u) * 2u;
   }
   const uint8_t* xa = reinterpret_cast<const uint8_t*>(p.a);
   const uint8_t* wb = reinterpret_cast<const uint8_t*>(p.bf16_weight);
   static_assert(NST >= S && S >= 2, "the ring is filled before the first stage");
+  static_assert((S - 2) * kDma < 64, "the ring's loads fit the vector memory count");
   auto issue = [&](auto J, uint32_t c) {
-    uint8_t* st = rt_stage<decltype(J)::value>();
+    uint8_t* st = rt_stage<decltype(J)::value, TM>();
 #pragma unroll
-    for (int i = 0; i < kRtDmaPerWave; ++i) {
-      const uint32_t g = wave * kRtDmaPerWave + i;  // wave-uniform
-      const uint8_t* src = (g < 8u ? xa : wb) + c * kRtRowBytes + g_off[i];
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(st + (g % 8u) * 1024u +
-                                                                                      (g < 8u ? 0u : kRtHalf)),
-                                       16, 0, 0);
+    for (int i = 0; i < kDma; ++i) {
+      const uint32_t g = wave * kDma + i;  // wave-uniform
+      const uint8_t* src = (g < kAGroups ? xa : wb) + c * kRtRowBytes + g_off[i];
+      __builtin_amdgcn_global_load_lds(
+          src, (__attribute__((address_space(3))) void*)(st + (g % kAGroups) * 1024u + (g < kAGroups ? 0u : kHalf)),
+          16, 0, 0);
     }
   };
 
@@ -142,32 +160,33 @@ __global__ __launch_bounds__(kRtThreads) void k_router_gemm(GroupedLaunch p) {
   const uint32_t lm = lane & 15u, kb = lane >> 4;
   const uint32_t s = rt_swz(lm);  // rows 16 b + lm have the swizzle of lm
   const uint32_t u0 = (kb ^ s) * 16u, u1 = ((4u | kb) ^ s) * 16u;
-  const uint32_t a_base = (32u * wm + lm) * kRtRowBytes;
-  const uint32_t b_base = kRtHalf + (32u * wn + lm) * kRtRowBytes;
-  // the bias of the lane's two output columns, loaded before the K loop
-  float bias[2];
+  const uint32_t a_base = (16u * kB * wm + lm) * kRtRowBytes;
+  const uint32_t b_base = kHalf + (16u * kB * wn + lm) * kRtRowBytes;
+  // the bias of the lane's output columns, loaded before the K loop
+  float bias[kB];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) bias[j] = p.bias != nullptr ? p.bias[col0 + 32u * wn + 16u * j + lm] : 0.0f;
-  f32x4_t acc[2][2];
+  for (int j = 0; j < kB; ++j) bias[j] = p.bias != nullptr ? p.bias[col0 + 16u * kB * wn + 16u * j + lm] : 0.0f;
+  f32x4_t acc[kB][kB];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < kB; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < kB; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](auto J) {
-    const uint8_t* st = rt_stage<decltype(J)::value>();
+    const uint8_t* st = rt_stage<decltype(J)::value, TM>();
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const uint32_t u = ks ? u1 : u0;
-      bf16x8_t a[2], b[2];
+      bf16x8_t a[kB], b[kB];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < kB; ++i) {
         a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_base + i * 16 * kRtRowBytes + u);
         b[i] = *reinterpret_cast<const bf16x8_t*>(st + b_base + i * 16 * kRtRowBytes + u);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < kB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < kB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
     }
   };
 
@@ -179,7 +198,7 @@ __global__ __launch_bounds__(kRtThreads) void k_router_gemm(GroupedLaunch p) {
   rt_unroll<0, NST>([&](auto C) {
     constexpr int c = decltype(C)::value;
     // this wave's loads of stage c are done once only the later stages' remain
-    wait_vm<(c + S - 2 < NST ? S - 2 : NST - 1 - c) * kRtDmaPerWave>();
+    wait_vm<(c + S - 2 < NST ? S - 2 : NST - 1 - c) * kDma>();
     wait_lgkm0();  // this wave's reads of stage c - 1 are done before its slot is refilled
     rt_barrier();  // every wave's loads of stage c have landed
     if constexpr (c + S - 1 < NST) issue(std::integral_constant<int, (c + S - 1) % S>{}, c + S - 1);
@@ -188,13 +207,13 @@ __global__ __launch_bounds__(kRtThreads) void k_router_gemm(GroupedLaunch p) {
 
   // lane holds C[4 (lane / 16) + q][lane % 16] of each 16 x 16 block
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const uint32_t col = col0 + 32u * wn + 16u * j + lm;
+  for (int j = 0; j < kB; ++j) {
+    const uint32_t col = col0 + 16u * kB * wn + 16u * j + lm;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < kB; ++i)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const uint32_t row = row0 + 32u * wm + 16u * i + 4u * kb + q;
+        const uint32_t row = row0 + 16u * kB * wm + 16u * i + 4u * kb + q;
         if (row < T) static_cast<float*>(p.out)[row * E + col] = round_bf16(acc[i][j][q] + bias[j]);
       }
   }
@@ -213,15 +232,30 @@ hipError_t rt_launch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_
 }  // namespace
 
 bool router_gemm_supported(uint32_t k_dim, uint32_t n_dim) {
-  return (k_dim == 1024 || k_dim == 2048 || k_dim == 4096) && n_dim % kRtCols == 0 && n_dim > 0;
+  return (k_dim == 1024 || k_dim == 2048 || k_dim == 4096) && n_dim % rt_tile<1>() == 0 && n_dim > 0;
 }
 
+#ifndef VM_ROUTER_BIG_TILE
+#define VM_ROUTER_BIG_TILE 1
+#endif
+
 template <int NST>
-hipError_t router_gemm_go(const GroupedLaunch& p, uint32_t blocks, bool one_per_cu, hipStream_t stream) {
-  // eight stages and one block per CU while the grid is at most one block per
-  // CU; above that four stages, two blocks per CU
-  if (one_per_cu) return rt_launch(k_router_gemm<8, NST>, dim3(blocks), dim3(kRtThreads), stream, p);
-  return rt_launch(k_router_gemm<4, NST>, dim3(blocks), dim3(kRtThreads), stream, p);
+hipError_t router_gemm_go(const GroupedLaunch& p, hipStream_t stream) {
+  auto blocks = [&](uint32_t tile) {
+    const uint32_t row_tiles = (p.rows + tile - 1) / tile, slices = p.n_dim / tile;
+    return std::make_pair(row_tiles * slices, (row_tiles + 7u) / 8u * 8u * slices);
+  };
+  // 128 x 128 tiles with four stages (one block per CU) once they still give
+  // every CU a block: half the L2 -> LDS traffic of 64 x 64 tiles, which
+  // re-read the rows once per 64 columns and the router rows once per 64 rows
+  const auto big = blocks(rt_tile<2>());
+  if (VM_ROUTER_BIG_TILE && p.n_dim % rt_tile<2>() == 0 && big.first >= 256u)
+    return rt_launch(k_router_gemm<4, NST, 2>, dim3(big.second), dim3(kRtThreads), stream, p);
+  // 64 x 64 tiles: eight stages and one block per CU while the grid is at
+  // most one block per CU; above that four stages, two blocks per CU
+  const auto small = blocks(rt_tile<1>());
+  if (small.first <= 256u) return rt_launch(k_router_gemm<8, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
+  return rt_launch(k_router_gemm<4, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
 }
 
 hipError_t launch_router_gemm(const GroupedLaunch& p, hipStream_t stream) {
@@ -229,13 +263,10 @@ hipError_t launch_router_gemm(const GroupedLaunch& p, hipStream_t stream) {
       static_cast<uint64_t>(p.rows) * p.k_dim * 2u > 0xffffffffull ||
       static_cast<uint64_t>(p.rows) * p.n_dim > 0xffffffffull || p.a_stride != p.k_dim)
     return hipErrorInvalidValue;
-  const uint32_t row_tiles = (p.rows + kRtRows - 1) / kRtRows, slices = p.n_dim / kRtCols;
-  const uint32_t blocks = (row_tiles + 7u) / 8u * 8u * slices;
-  const bool one_per_cu = row_tiles * slices <= 256u;
   switch (p.k_dim) {
-    case 1024: return router_gemm_go<1024 / kRtK>(p, blocks, one_per_cu, stream);
-    case 2048: return router_gemm_go<2048 / kRtK>(p, blocks, one_per_cu, stream);
-    default: return router_gemm_go<4096 / kRtK>(p, blocks, one_per_cu, stream);
+    case 1024: return router_gemm_go<1024 / kRtK>(p, stream);
+    case 2048: return router_gemm_go<2048 / kRtK>(p, stream);
+    default: return router_gemm_go<4096 / kRtK>(p, stream);
   }
 }
 
