@@ -238,6 +238,13 @@ bool router_gemm_supported(uint32_t k_dim, uint32_t n_dim) {
 #ifndef VM_ROUTER_BIG_TILE
 #define VM_ROUTER_BIG_TILE 1
 #endif
+// Ring depths: 64 x 64 tiles at one block per CU, and 128 x 128 tiles.
+#ifndef VM_ROUTER_STAGES_1
+#define VM_ROUTER_STAGES_1 8
+#endif
+#ifndef VM_ROUTER_STAGES_2
+#define VM_ROUTER_STAGES_2 4
+#endif
 
 template <int NST>
 hipError_t router_gemm_go(const GroupedLaunch& p, hipStream_t stream) {
@@ -250,11 +257,11 @@ hipError_t router_gemm_go(const GroupedLaunch& p, hipStream_t stream) {
   // re-read the rows once per 64 columns and the router rows once per 64 rows
   const auto big = blocks(rt_tile<2>());
   if (VM_ROUTER_BIG_TILE && p.n_dim % rt_tile<2>() == 0 && big.first >= 256u)
-    return rt_launch(k_router_gemm<4, NST, 2>, dim3(big.second), dim3(kRtThreads), stream, p);
+    return rt_launch(k_router_gemm<VM_ROUTER_STAGES_2, NST, 2>, dim3(big.second), dim3(kRtThreads), stream, p);
   // 64 x 64 tiles: eight stages and one block per CU while the grid is at
   // most one block per CU; above that four stages, two blocks per CU
   const auto small = blocks(rt_tile<1>());
-  if (small.first <= 256u) return rt_launch(k_router_gemm<8, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
+  if (small.first <= 256u) return rt_launch(k_router_gemm<VM_ROUTER_STAGES_1, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
   return rt_launch(k_router_gemm<4, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
 }
 
