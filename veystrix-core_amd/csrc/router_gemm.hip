@@ -261,7 +261,8 @@ hipError_t router_gemm_go(const GroupedLaunch& p, hipStream_t stream) {
   // 64 x 64 tiles: eight stages and one block per CU while the grid is at
   // most one block per CU; above that four stages, two blocks per CU
   const auto small = blocks(rt_tile<1>());
-  if (small.first <= 256u) return rt_launch(k_router_gemm<VM_ROUTER_STAGES_1, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
+  if (small.first <= 256u)
+    return rt_launch(k_router_gemm<VM_ROUTER_STAGES_1, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
   return rt_launch(k_router_gemm<4, NST, 1>, dim3(small.second), dim3(kRtThreads), stream, p);
 }
 
