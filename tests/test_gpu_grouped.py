@@ -105,25 +105,28 @@ def test_grouped_layer_many_rows_per_expert(device):
     _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, "grouped layer T=2048 (sample)")
 
 
-@pytest.mark.parametrize("hidden,experts,tokens", [(4096, 128, 300), (4096, 128, 8256), (1024, 512, 4096)],
-                         ids=["k4096-8stage", "k4096-4stage", "k1024-4stage"])
-def test_router_gemm_instances(device, hidden, experts, tokens):
+@pytest.mark.parametrize("hidden,experts,tokens,zipf", [(4096, 128, 300, None), (4096, 128, 8256, None),
+                                                         (1024, 512, 4096, None), (2048, 512, 1000, 1.1)],
+                         ids=["k4096-8stage", "k4096-4stage", "k1024-4stage", "k2048-bias"])
+def test_router_gemm_instances(device, hidden, experts, tokens, zipf):
     """The router GEMM of calls above 64 rows at the K and ring depths the
     prefill shapes do not reach (K = 4096 with eight and four stages, K = 1024
-    with four): the experts chosen per row equal the decode router's, which
-    sums every logit in another order, except on near ties (bounded, and
-    checked against the oracle's gates); at 300 rows the whole layer is
+    with four) and with a router bias (the log-Zipf popularity of the
+    synthetic layers): the experts chosen per row equal the decode router's,
+    which sums every logit in another order, except on near ties (bounded,
+    and checked against the oracle's gates); at 300 rows the whole layer is
     compared with the oracle."""
     from veymoe.router import router_topk
 
-    spec = synth.LayerSpec(f"router_k{hidden}", hidden, 256, experts, 6, 0, tokens)
+    spec = synth.LayerSpec(f"router_k{hidden}", hidden, 256, experts, 6, 0, tokens, zipf_s=zipf)
     seed = 340 + hidden // 1024 + experts
     layer = assemble.build_layer(spec, seed, device, dense=True)
     x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
     x = bf16_device(x_np, device)
     y = layer(x)
     grouped = layer.last_inds.sort(dim=1).values
-    decode, _ = router_topk(x, layer.gate.weight, spec.top_k)
+    bias = layer.gate.bias.float() if layer.gate.bias is not None else None
+    decode, _ = router_topk(x, layer.gate.weight, spec.top_k, logit_bias=bias)
     decode = decode.sort(dim=1).values
     torch.cuda.synchronize()
     differ = np.nonzero(~(grouped == decode).all(dim=1).cpu().numpy())[0]
