@@ -106,13 +106,15 @@ def test_grouped_layer_many_rows_per_expert(device):
 
 
 @pytest.mark.parametrize("hidden,experts,tokens,zipf", [(4096, 128, 300, None), (4096, 128, 8256, None),
-                                                         (1024, 512, 4096, None), (2048, 512, 1000, 1.1)],
-                         ids=["k4096-8stage", "k4096-4stage", "k1024-4stage", "k2048-bias"])
+                                                         (1024, 512, 4096, None), (2048, 512, 1000, 1.1),
+                                                         (1024, 96, 300, None)],
+                         ids=["k4096-8stage", "k4096-4stage", "k1024-4stage", "k2048-bias", "chunked-e96"])
 def test_router_gemm_instances(device, hidden, experts, tokens, zipf):
     """The router GEMM of calls above 64 rows at the K and ring depths the
     prefill shapes do not reach (K = 4096 with eight and four stages, K = 1024
-    with four) and with a router bias (the log-Zipf popularity of the
-    synthetic layers): the experts chosen per row equal the decode router's,
+    with four), with a router bias (the log-Zipf popularity of the
+    synthetic layers), and at 96 experts, which the ring does not take (the
+    chunked GEMM computes those logits): the experts chosen per row equal the decode router's,
     which sums every logit in another order, except on near ties (bounded,
     and checked against the oracle's gates); at 300 rows the whole layer is
     compared with the oracle."""
