@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define VM_ABI_VERSION 2
+#define VM_ABI_VERSION 3
 
 /* status codes (0 = ok) */
 #define VM_OK 0
@@ -216,6 +216,13 @@ typedef struct VmLayerArgs {
    * expert_cache.py:1434-1443; adaptive_topk.py:271-278).  Grouped calls
    * always combine generically. */
   uint32_t combine;
+  /* Optional [tokens, expert_count] activation dtype: the softmax gates of
+   * every expert, written by router-only calls (phases == VM_PHASE_ROUTER).
+   * The host's adaptive top-k (adaptive_topk.py:76-235) reads the selected
+   * experts' gates from here before it rewrites the routes for the experts
+   * call.  No counterpart in the reference's C surface: MLX hands the host
+   * the gates array itself. */
+  void* gates_out;
 } VmLayerArgs;
 #define VM_COMBINE_FUSED 0u
 #define VM_COMBINE_GENERIC 1u

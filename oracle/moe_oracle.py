@@ -227,6 +227,78 @@ def route(x, router_bits, k, mode, logit_bias=None, blend=1.0):
     return inds, renorm(scores, mode, blend), gates
 
 
+def keep_for_mass(weights, threshold):
+    """adaptive_topk.py:44-51: the first 1-based position at which the running
+    sum of weight / total reaches ``threshold``; len(weights) otherwise."""
+    total = sum(weights)
+    running = 0.0
+    for i in range(len(weights)):
+        running += weights[i] / total
+        if running >= threshold:
+            return i + 1
+    return len(weights)
+
+
+def swap_row(experts, weights, keep, resident, epsilon):
+    """adaptive_topk.py:397-431: each cold kept slot, lightest first, swaps
+    with the heaviest resident dropped slot within ``epsilon`` below it that
+    no earlier slot took."""
+    spare = [i for i in range(keep, len(experts)) if resident(experts[i])]
+    cold = [i for i in range(keep) if not resident(experts[i])]
+    if not spare or not cold:
+        return list(experts), list(weights)
+    experts, weights = list(experts), list(weights)
+    used = []
+    for i in sorted(cold, key=lambda j: weights[j]):
+        choice = -1
+        for j in spare:
+            if j in used or weights[i] - weights[j] > epsilon:
+                continue
+            if choice < 0 or weights[j] > weights[choice]:
+                choice = j
+        if choice >= 0:
+            used.append(choice)
+            experts[i], experts[choice] = experts[choice], experts[i]
+            weights[i], weights[choice] = weights[choice], weights[i]
+    return experts, weights
+
+
+def adaptive_routes(inds, gates_k, threshold, mode, min_keep=1, blend=1.0, resident=None, swap=None,
+                    epsilon=0.02):
+    """The adaptive top-k of adaptive_topk.py:76-235 and the renorm of :257-262.
+
+    ``inds``/``gates_k`` [T, k]: the top-k experts and their (rounded) gates.
+    Rows are ordered by gate descending; keep = max(min(k, min_keep), the mass
+    rule); ``swap(expert) -> bool`` enables the cache-aware swap; ``resident``
+    (a set) keeps dropped slots of resident experts.  Disabled slots take the
+    row's first expert and score 0; the result is cut to the widest row.
+    Returns (inds [T, width], scores [T, width], keeps)."""
+    inds = np.asarray(inds)
+    gates_k = np.asarray(gates_k, dtype=np.float32)
+    t, k = inds.shape
+    expert_rows, weight_rows, keeps = [], [], []
+    floor = max(1, min(k, min_keep))
+    for r in range(t):
+        order = sorted(range(k), key=lambda j: -float(gates_k[r, j]))
+        e = [int(inds[r, j]) for j in order]
+        w = [float(gates_k[r, j]) for j in order]
+        keep = max(floor, keep_for_mass(w, threshold))
+        if swap is not None:
+            e, w = swap_row(e, w, keep, swap, epsilon)
+        expert_rows.append(e)
+        weight_rows.append(w)
+        keeps.append(keep)
+    enabled = [[j < keeps[r] or (resident is not None and expert_rows[r][j] in resident) for j in range(k)]
+               for r in range(t)]
+    width = max(j + 1 for r in range(t) for j in range(k) if enabled[r][j])
+    out_inds = np.array([[expert_rows[r][j] if enabled[r][j] else expert_rows[r][0] for j in range(width)]
+                         for r in range(t)], dtype=np.int32)
+    kept = np.array([[weight_rows[r][j] if enabled[r][j] else 0.0 for j in range(width)] for r in range(t)],
+                    dtype=np.float32)
+    topk_mass = _round(gates_k.astype(np.float64).sum(axis=-1, keepdims=True), mode)
+    return out_inds, renorm(kept, mode, blend, topk_mass), [sum(row) for row in enabled]
+
+
 # --------------------------------------------------------------------------
 # Experts and combine.
 
@@ -373,7 +445,7 @@ def decode_combine(layer_id):
     return "generic" if layer_id == 0 else "fused"
 
 
-def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None, combine=None):
+def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None, combine=None, adaptive=None):
     """One MoE layer.  ``layer`` holds numpy arrays (see veymoe.synth).
 
     path "decode": rows <= 8, vector-form projections, and the combine of
@@ -381,7 +453,9 @@ def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None, co
     (adaptive_topk.py:289-293), or the generic one for layer 0;
     path "prefill": generic combine (adaptive_topk.py:275-278), matrix-form
     projections (gather_qmm, weights rounded) unless ``qmm`` says otherwise.
-    ``combine`` ("fused"/"generic") overrides the rule.
+    ``combine`` ("fused"/"generic") overrides the rule.  ``adaptive``: keyword
+    arguments of ``adaptive_routes`` (threshold, min_keep, ...) applied to the
+    top-k before the experts.
     Returns dict(inds, scores, gates, output, down, shared, shared_gate)."""
     x = np.asarray(x, dtype=np.float32)
     if qmm is None:
@@ -390,6 +464,9 @@ def moe_layer(x, layer, mode, path="decode", group_size=GROUP_SIZE, qmm=None, co
         combine = decode_combine(layer.get("layer_id")) if path == "decode" else "generic"
     k = int(layer["top_k"])
     inds, scores, gates = route(x, layer["router"], k, mode, layer.get("router_bias"))
+    if adaptive is not None:
+        inds, scores, _ = adaptive_routes(inds, np.take_along_axis(gates, inds, axis=-1), mode=mode, **adaptive)
+        k = inds.shape[1]
     shared, shared_gate = shared_expert(x, layer, mode, group_size, qmm)
     projections = {name: layer[name] for name in ("gate_proj", "up_proj", "down_proj")}
     tokens = x.shape[0]

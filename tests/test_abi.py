@@ -26,7 +26,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert set(names) == set(_lib.SIGNATURES)
-    assert lib.vm_abi_version() == 2
+    assert lib.vm_abi_version() == 3
 
 
 def test_struct_layouts_match_the_header(tmp_path):

@@ -590,8 +590,13 @@ uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden
                                 uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype) {
   if (use_grouped(tokens, act_dtype))
     return grouped_ws(tokens, top_k, hidden_size, inter_size, expert_count, shared_inter != 0).total;
-  const uint32_t chunk = tokens < VM_LAYER_MAX_TOKENS ? tokens : VM_LAYER_MAX_TOKENS;
-  return layer_ws(chunk, top_k, inter_size, shared_inter, expert_count, act_dtype).total;
+  if (tokens <= VM_LAYER_MAX_TOKENS) return layer_ws(tokens, top_k, inter_size, shared_inter, expert_count, act_dtype).total;
+  // fp32 above the decode bound: one decode workspace per chunk of
+  // VM_LAYER_MAX_TOKENS rows, so that a router-only call leaves every chunk's
+  // routes and shared gate for the experts-only call
+  const uint64_t per = align_up(layer_ws(VM_LAYER_MAX_TOKENS, top_k, inter_size, shared_inter, expert_count,
+                                         act_dtype).total);
+  return per * ((tokens + VM_LAYER_MAX_TOKENS - 1) / VM_LAYER_MAX_TOKENS);
 }
 
 static int layer_decode(const VmLayerArgs* a, hipStream_t stream);
@@ -648,11 +653,19 @@ int vm_moe_layer(const VmLayerArgs* a, void* stream_ptr) {
   if (T <= VM_LAYER_MAX_TOKENS) return layer_decode(a, stream);
   // fp32 activations above the decode bound: decode kernels in chunks of
   // VM_LAYER_MAX_TOKENS tokens (with no rounding the fused and the generic
-  // combine agree)
+  // combine agree), each chunk in a workspace slice of its own
+  const uint64_t per = align_up(layer_ws(VM_LAYER_MAX_TOKENS, K, a->inter_size, a->shared_inter, a->expert_count,
+                                         a->act_dtype).total);
+  const uint64_t need = per * ((T + VM_LAYER_MAX_TOKENS - 1) / VM_LAYER_MAX_TOKENS);
+  if (a->workspace == nullptr || a->workspace_bytes < need)
+    return fail(VM_EWORKSPACE, "workspace of %llu bytes needed", (unsigned long long)need);
   for (uint32_t t0 = 0; t0 < T; t0 += VM_LAYER_MAX_TOKENS) {
     VmLayerArgs c = *a;
     const uint32_t n = T - t0 < VM_LAYER_MAX_TOKENS ? T - t0 : VM_LAYER_MAX_TOKENS;
     c.tokens = n;
+    c.workspace = static_cast<char*>(a->workspace) + per * (t0 / VM_LAYER_MAX_TOKENS);
+    c.workspace_bytes = per;
+    if (a->gates_out != nullptr) c.gates_out = static_cast<float*>(a->gates_out) + uint64_t(t0) * a->expert_count;
     c.x = static_cast<const float*>(a->x) + uint64_t(t0) * H;
     c.output = static_cast<float*>(a->output) + uint64_t(t0) * H;
     if (a->inds_out != nullptr) c.inds_out = a->inds_out + uint64_t(t0) * K;
@@ -780,6 +793,7 @@ static int layer_decode(const VmLayerArgs* a, hipStream_t stream) {
       s.top_k = K;
       s.act_dtype = static_cast<int>(a->act_dtype);
       s.blend = a->renorm_blend;
+      s.gates = phases == VM_PHASE_ROUTER ? a->gates_out : nullptr;
       e = vm::launch_select(s, stream);
       if (e != hipSuccess) return hip_fail(e, "select launch");
     }
@@ -1284,6 +1298,7 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     s.top_k = K;
     s.act_dtype = VM_BF16;
     s.blend = a->renorm_blend;
+    s.gates = phases == VM_PHASE_ROUTER ? a->gates_out : nullptr;
     e = vm::launch_select(s, stream);
     if (e != hipSuccess) return done(hip_fail(e, "select launch"));
   }

@@ -112,6 +112,7 @@ class VmLayerArgs(ctypes.Structure):
         ("inject_out", _vp),
         ("hc_count", _c_u32),
         ("combine", _c_u32),
+        ("gates_out", _vp),
     ]
 
 

@@ -30,7 +30,7 @@ from typing import Optional
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, adaptive
 from .device import act_code, ptr, q4proj, require_device, stream_handle
 from .executor import HipMoEExecutor, Q4G32Projection, _as_projection
 from .layout import RecordLayout
@@ -304,22 +304,58 @@ class MoELayer:
             _lib.check(lib.vm_moe_layer_lru(args, lru.view(sw.layer_id), stream_handle()))
             self.last_inds, self.last_scores = inds, scores
             return out
+        if adaptive.threshold_for(self._flashnext_layer_id) < 1.0:
+            return self._forward_adaptive(args, inds, scores, flat, out)
         if sw.pool is not None and not sw._pool_fully_resident():
             # router, then the host LRU pass on synced routes, then the experts
             args.phases = _lib.VM_PHASE_ROUTER
             _lib.check(lib.vm_moe_layer(args, stream_handle()))
-            routed = self._routes_to_host(inds)
-            wanted = list(dict.fromkeys(routed))
-            slots, misses = sw.pool.assign(sw.layer_id, wanted)
-            sw.hits += len(routed) - len(misses)
-            sw.misses += len(misses)
-            if misses:
-                if sw.host_store is None:
-                    sw.pool.invalidate(sw.layer_id, misses)
-                    raise RuntimeError("expert pool miss with no host record store to fill from")
-                sw.pool.fill(sw.layer_id, misses, sw.host_store)
-            sw.pool.sync_tables()
+            self._host_lru_pass(self._routes_to_host(inds))
             args.phases = _lib.VM_PHASE_EXPERTS
+        _lib.check(lib.vm_moe_layer(args, stream_handle()))
+        self.last_inds, self.last_scores = inds, scores
+        return out
+
+    def _host_lru_pass(self, routed: list) -> None:
+        """assign() of the routed ids in first-seen order, staging the misses
+        from the host record store (expert_cache.py:1842-1947)."""
+        sw = self.switch_mlp
+        wanted = list(dict.fromkeys(routed))
+        slots, misses = sw.pool.assign(sw.layer_id, wanted)
+        sw.hits += len(routed) - len(misses)
+        sw.misses += len(misses)
+        if misses:
+            if sw.host_store is None:
+                sw.pool.invalidate(sw.layer_id, misses)
+                raise RuntimeError("expert pool miss with no host record store to fill from")
+            sw.pool.fill(sw.layer_id, misses, sw.host_store)
+        sw.pool.sync_tables()
+
+    def _forward_adaptive(self, args, inds: torch.Tensor, scores: torch.Tensor, flat: torch.Tensor,
+                          out: torch.Tensor) -> torch.Tensor:
+        """A threshold below 1.0 (adaptive_topk.py:76-262): a router-only call
+        that also writes the gates, the host plan of ``veymoe.adaptive``, the
+        pool's host LRU pass on the planned routes, and an experts-only call
+        on them.  The experts call keeps all top_k slots: dropped slots route
+        to the row's first expert with score 0 and add nothing."""
+        lib = _lib.lib()
+        sw = self.switch_mlp
+        gates = torch.empty((flat.shape[0], sw.num_experts), dtype=flat.dtype, device=flat.device)
+        args.phases = _lib.VM_PHASE_ROUTER
+        args.gates_out = ptr(gates)
+        try:
+            _lib.check(lib.vm_moe_layer(args, stream_handle()))
+        finally:
+            args.gates_out = None
+        picked = torch.gather(gates, 1, inds.long()).float().cpu().numpy()
+        new_inds, new_scores, _, width = adaptive.plan(self._flashnext_layer_id, inds.cpu().numpy(), picked,
+                                                       self.renorm_blend, bf16=flat.dtype == torch.bfloat16)
+        inds.copy_(torch.from_numpy(new_inds))
+        scores.copy_(torch.from_numpy(new_scores).to(scores.dtype))
+        if sw.pool is not None and not sw._pool_fully_resident():
+            # the routes the reference's expert block receives: cut to the width
+            self._host_lru_pass(new_inds[:, :width].reshape(-1).tolist())
+        args.phases = _lib.VM_PHASE_EXPERTS
         _lib.check(lib.vm_moe_layer(args, stream_handle()))
         self.last_inds, self.last_scores = inds, scores
         return out
