@@ -122,3 +122,16 @@ def test_observer_sees_rows_before_the_swap():
     inds, g = _rows(rng, 5, 4, 16)
     adaptive.plan(2, inds, g)
     assert len(seen) == 1 and seen[0][0] == 2 and len(seen[0][1]) == 2 and len(seen[0][3]) == 2
+
+
+def test_exact_routing_reports_every_slot_to_the_observer():
+    seen = []
+    assert not adaptive.observing()
+    adaptive.set_route_observer(lambda layer, e, w, k: seen.append((layer, e, w, k)))
+    assert adaptive.observing()
+    inds = np.array([[3, 1, 2], [5, 4, 0]], np.int32)
+    gates = np.array([[0.5, 0.25, 0.25], [0.75, 0.125, 0.125]], np.float32)
+    adaptive.observe_exact(7, inds, gates)
+    assert seen == [(7, inds.tolist(), gates.tolist(), [3, 3])]
+    adaptive.observe_exact(None, inds, gates)   # no layer id: nothing
+    assert len(seen) == 1

@@ -22,6 +22,7 @@ def _reset():
     adaptive.set_threshold(1.0)
     adaptive.set_min_keep(1)
     adaptive.set_resident_experts()
+    adaptive.set_route_observer()
     adaptive.reset_keep_stats()
 
 
@@ -111,3 +112,19 @@ def test_fp32_split_path_above_the_decode_bound(device):
     assert torch.equal(c, d)
     ref = mo.moe_layer(x.cpu().numpy(), synth.numpy_layer(SPEC, seed), "f32", adaptive=dict(threshold=0.6))
     assert_close(host(d), ref["output"], "adaptive fp32 chunks", rtol=1e-3, atol=1e-4, max_rel=1e-3)
+
+
+def test_route_observer_at_threshold_one_leaves_the_routes(device):
+    """An observer at the default threshold sees each call's routes with keep
+    k, and the layer's output is the plain one."""
+    seed = 437
+    layer = assemble.build_layer(SPEC, seed, device, dense=True)
+    x = assemble.tokens_tensor(SPEC, seed, device, 3)
+    plain = layer(x)
+    plain_inds = layer.last_inds.clone()
+    seen = []
+    adaptive.set_route_observer(lambda l, e, w, k: seen.append((l, e, w, k)))
+    observed = layer(x)
+    assert torch.equal(plain.view(torch.int16), observed.view(torch.int16))
+    assert len(seen) == 1 and seen[0][0] == 0 and seen[0][3] == [SPEC.top_k] * 3
+    assert seen[0][1] == plain_inds.cpu().tolist()

@@ -90,6 +90,21 @@ def threshold_for(layer: Optional[int]) -> float:
     return _layer_thresholds.get(layer, _threshold)
 
 
+def observing() -> bool:
+    """A route observer is set: it sees every call's routes, at threshold 1.0
+    too (adaptive_topk.py:240-253)."""
+    return _observer is not None
+
+
+def observe_exact(layer: Optional[int], inds: np.ndarray, gates: np.ndarray) -> None:
+    """Threshold 1.0 with an observer: every row keeps all k slots."""
+    if _observer is None or layer is None:
+        return
+    rows, k = np.asarray(inds).shape
+    n = rows if _observer_max_rows is None else min(rows, _observer_max_rows)
+    _observer(layer, np.asarray(inds)[:n].tolist(), np.asarray(gates)[:n].tolist(), [k] * n)
+
+
 def last_keeps() -> Dict[int, Tuple[int, ...]]:
     return dict(_last_keeps)
 

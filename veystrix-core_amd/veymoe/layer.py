@@ -304,7 +304,7 @@ class MoELayer:
             _lib.check(lib.vm_moe_layer_lru(args, lru.view(sw.layer_id), stream_handle()))
             self.last_inds, self.last_scores = inds, scores
             return out
-        if adaptive.threshold_for(self._flashnext_layer_id) < 1.0:
+        if adaptive.threshold_for(self._flashnext_layer_id) < 1.0 or adaptive.observing():
             return self._forward_adaptive(args, inds, scores, flat, out)
         if sw.pool is not None and not sw._pool_fully_resident():
             # router, then the host LRU pass on synced routes, then the experts
@@ -337,7 +337,9 @@ class MoELayer:
         that also writes the gates, the host plan of ``veymoe.adaptive``, the
         pool's host LRU pass on the planned routes, and an experts-only call
         on them.  The experts call keeps all top_k slots: dropped slots route
-        to the row's first expert with score 0 and add nothing."""
+        to the row's first expert with score 0 and add nothing.  At threshold
+        1.0 with a route observer set, the observer sees the routes and they
+        stay as selected (adaptive_topk.py:240-253)."""
         lib = _lib.lib()
         sw = self.switch_mlp
         gates = torch.empty((flat.shape[0], sw.num_experts), dtype=flat.dtype, device=flat.device)
@@ -348,13 +350,21 @@ class MoELayer:
         finally:
             args.gates_out = None
         picked = torch.gather(gates, 1, inds.long()).float().cpu().numpy()
-        new_inds, new_scores, _, width = adaptive.plan(self._flashnext_layer_id, inds.cpu().numpy(), picked,
-                                                       self.renorm_blend, bf16=flat.dtype == torch.bfloat16)
-        inds.copy_(torch.from_numpy(new_inds))
-        scores.copy_(torch.from_numpy(new_scores).to(scores.dtype))
-        if sw.pool is not None and not sw._pool_fully_resident():
+        host_inds = inds.cpu().numpy()
+        layer = self._flashnext_layer_id
+        if adaptive.threshold_for(layer) >= 1.0:
+            # exact routing with a route observer: it sees the routes, which stay
+            adaptive.observe_exact(layer, host_inds, picked)
+            routed = host_inds.reshape(-1).tolist()
+        else:
+            new_inds, new_scores, _, width = adaptive.plan(layer, host_inds, picked, self.renorm_blend,
+                                                           bf16=flat.dtype == torch.bfloat16)
+            inds.copy_(torch.from_numpy(new_inds))
+            scores.copy_(torch.from_numpy(new_scores).to(scores.dtype))
             # the routes the reference's expert block receives: cut to the width
-            self._host_lru_pass(new_inds[:, :width].reshape(-1).tolist())
+            routed = new_inds[:, :width].reshape(-1).tolist()
+        if sw.pool is not None and not sw._pool_fully_resident():
+            self._host_lru_pass(routed)
         args.phases = _lib.VM_PHASE_EXPERTS
         _lib.check(lib.vm_moe_layer(args, stream_handle()))
         self.last_inds, self.last_scores = inds, scores
