@@ -190,3 +190,28 @@ def test_a_queue_with_a_foreign_slot_leaves_the_state_untouched(device):
     assert int(status.item()) & 16
     for b, t in zip(before, (pool.slot_table, lru.slot_owner, lru.lru_order, lru.counters)):
         assert torch.equal(b, t)
+
+
+def test_adaptive_threshold_hands_the_state_back(device):
+    """Below threshold 1.0 the plan runs on the host (adaptive_topk.py:76-235):
+    a layer with a device LRU hands the state back for the call, gives the
+    dense layer's bits (both planned), and its slot table follows the planned
+    routes cut to the widest row."""
+    from veymoe import adaptive
+
+    layers, slots = 1, 48
+    store, pool, pooled, dense = _setup(device, SMALL, layers, slots)
+    ref = pool_oracle.LruSlots(slots)
+    pool.attach_device_lru(store)
+    adaptive.set_threshold(0.6)
+    try:
+        for step, tokens in enumerate([1, 3, 1, 2]):
+            routed = _step(SMALL, pooled, dense, 0, tokens, 500 + step, device)
+            width = max(adaptive.last_keeps()[0])
+            planned = np.asarray(routed).reshape(tokens, SMALL.top_k)[:, :width].reshape(-1).tolist()
+            ref.assign(0, planned)
+            assert pool.device_lru is not None
+    finally:
+        adaptive.set_threshold(1.0)
+    table = pool.device_lru.state()[0]
+    np.testing.assert_array_equal(table, _expected_table(ref, layers, SMALL.experts))

@@ -290,9 +290,10 @@ class MoELayer:
         sw = self.switch_mlp
         lru = sw.pool.device_lru if sw.pool is not None else None
         if lru is not None:
-            if tokens > MAX_DECODE_ROWS:
-                # the grouped path resolves its experts on the host: hand the
-                # LRU state back for this call
+            if tokens > MAX_DECODE_ROWS or adaptive.threshold_for(self._flashnext_layer_id) < 1.0 or \
+                    adaptive.observing():
+                # the grouped path and the adaptive plan resolve their
+                # experts on the host: hand the LRU state back for this call
                 sw.pool.detach_device_lru()
                 try:
                     return self.forward(flat, inject)
