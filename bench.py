@@ -121,9 +121,11 @@ def algorithmic_bytes(spec):
             "front": front, "experts": experts, "gateup_routed": gateup_routed}
 
 
-def cpu_baseline(spec, seed, seconds):
+def cpu_baseline(spec, seed, seconds, min_runs=20, warmup=3):
     """The C restatement on a bounded sample: one layer of the same shape,
-    decode tokens until ``seconds`` of CPU work."""
+    one decode token per timed run, ``warmup`` untimed runs first, then runs
+    until ``seconds`` of CPU work and at least ``min_runs`` runs; the rate is
+    one over the median run."""
     import numpy as np
 
     from oracle.build import LIB, build
@@ -145,19 +147,22 @@ def cpu_baseline(spec, seed, seconds):
                          records, layout.record_stride, layout.part_offsets(),
                          shared=synth.shared_parts(spec, seed, 0))
     xs = synth.tokens(spec, seed, 64)
-    layer.run(xs[0])
-    count = 0
+    for i in range(warmup):
+        layer.run(xs[i % len(xs)])
+    runs = []
     start = time.perf_counter()
-    while True:
-        layer.run(xs[count % len(xs)])
-        count += 1
-        elapsed = time.perf_counter() - start
-        if elapsed >= seconds:
-            break
-    return {"value": round(count / elapsed, 2), "unit": "tok/s", "cores": threads(), "kind": "port",
-            "nproc": os.cpu_count(), "cpu_model": cpu_model(),
-            "sample": f"{count} decode tokens through one layer of the same shape ({elapsed:.1f} s), "
-                      f"C restatement oracle/cmoe.c with OpenMP on {threads()} threads"}
+    while len(runs) < min_runs or time.perf_counter() - start < seconds:
+        t0 = time.perf_counter()
+        layer.run(xs[len(runs) % len(xs)])
+        runs.append(time.perf_counter() - t0)
+    elapsed = time.perf_counter() - start
+    median = float(np.median(runs))
+    return {"value": round(1.0 / median, 2), "unit": "tok/s", "cores": threads(), "kind": "port",
+            "nproc": os.cpu_count(), "threads_used": threads(), "cpu_model": cpu_model(),
+            "median_ms_per_token": round(median * 1e3, 4), "runs": len(runs),
+            "sample": f"{len(runs)} timed decode tokens through one layer of the same shape after {warmup} "
+                      f"warm-up tokens ({elapsed:.1f} s), rate = 1 / median run; C restatement oracle/cmoe.c "
+                      f"with OpenMP on {threads()} threads of {os.cpu_count()} visible cores"}
 
 
 def cpu_model():

@@ -209,12 +209,15 @@ def renorm(scores, mode, blend=1.0, topk_mass=None):
     """``scores / (topk_mass + blend*(selected_mass - topk_mass))``.
 
     With the full top-k selected, selected_mass == topk_mass, so the result is
-    ``scores / sum(scores)``; every step is rounded in bf16 mode."""
+    ``scores / sum(scores)``; every step is rounded in bf16 mode, blend
+    included: compiled.py:111 makes it ``mx.array(blend, scores.dtype)``, and
+    the plain form (adaptive_topk.py:260-261) multiplies a bf16 array by a
+    Python float, which MLX casts to the array's type."""
     scores = np.asarray(scores, dtype=np.float32)
     selected = _round(scores.astype(np.float64).sum(axis=-1, keepdims=True), mode)
     mass = selected if topk_mass is None else topk_mass
     diff = _round(selected - mass, mode)
-    normalizer = _round(mass + _round(np.float32(blend) * diff, mode), mode)
+    normalizer = _round(mass + _round(_round(np.float32(blend), mode) * diff, mode), mode)
     return _round(scores.astype(np.float64) / normalizer.astype(np.float64), mode)
 
 

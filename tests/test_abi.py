@@ -226,3 +226,22 @@ def test_static_layer_refuses_calls_above_its_scratch_without_a_device():
     assert lib.vm_moe_layer_workspace(8, 10, 2048, 512, 0, 512, 0) <= _lib.VM_STATIC_SCRATCH_BYTES
     a.router_weight = 770
     assert lib.vm_moe_layer_static(ctypes.byref(a), None) == _lib.VM_EINVAL
+
+
+def test_decode_workspace_reserves_hand_off_words_for_one_token_bf16_only():
+    """fp32 calls above the decode bound take one decode workspace per chunk
+    of 8 rows.  Laid out by hand at 8 rows, hidden 2048, top-10 of 512, inter
+    512 with a shared expert (offsets 256-aligned): logits 8*512*4 = 16384 B,
+    activations 8*11*512*4 = 180224 B, sigmoid 32 -> 256, indices, scores and
+    route words 320 -> 512 each, the LRU fill list 4 + 8*80 = 644 -> 768, after
+    a 256-byte head: 199424 B, with no hand-off words (those serve one-token
+    bf16 calls only).  2048 fp32 rows: 256 such chunks, 48.7 MiB."""
+    lib = _lib.lib()
+    per = lib.vm_moe_layer_workspace(8, 10, 2048, 512, 512, 512, 1)
+    assert per == 199424
+    assert lib.vm_moe_layer_workspace(2048, 10, 2048, 512, 512, 512, 1) == 256 * 199424
+    # one bf16 token: its own sizes plus the pipeline's tag words (one 32-bit
+    # word per activation of the ten routed slots at least)
+    one = lib.vm_moe_layer_workspace(1, 10, 2048, 512, 512, 512, 0)
+    one_f32 = lib.vm_moe_layer_workspace(1, 10, 2048, 512, 512, 512, 1)
+    assert one - one_f32 >= 10 * 512 * 4 - 11 * 512 * 2

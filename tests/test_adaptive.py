@@ -135,3 +135,90 @@ def test_exact_routing_reports_every_slot_to_the_observer():
     assert seen == [(7, inds.tolist(), gates.tolist(), [3, 3])]
     adaptive.observe_exact(None, inds, gates)   # no layer id: nothing
     assert len(seen) == 1
+
+
+# The reference's own known answers for swap_row (models/flashnext/tests/unit/
+# test_swap_routing.py:25-81), restated as data: (experts, weights, keep,
+# resident experts, epsilon) -> the expected experts, and the weights checked
+# there.  The product returns its input list itself when nothing moves
+# (the reference asserts identity, :42-54).
+_REF_SWAP_CASES = [
+    # a cold pick takes a close resident spare (:25-30)
+    ([1, 7, 9], [0.5, 0.021, 0.019], 2, {1, 9}, 0.02, [1, 9, 7], {1: 0.019}),
+    # a distant spare is left alone (:32-36)
+    ([1, 7, 9], [0.5, 0.021, 0.001], 2, {1, 9}, 0.005, [1, 7, 9], {}),
+    # nothing moves when every pick is resident (:38-43)
+    ([1, 7, 9], [0.5, 0.021, 0.019], 2, {1, 7, 9}, 0.02, [1, 7, 9], {}),
+    # nothing moves when no spare is resident (:45-50)
+    ([1, 7, 9], [0.5, 0.021, 0.019], 2, {1}, 0.02, [1, 7, 9], {}),
+    # it keeps the strongest spare (:59-64)
+    ([7, 9, 10], [0.030, 0.029, 0.011], 1, {9, 10}, 0.05, [9, 7, 10], {0: 0.029}),
+]
+
+
+@pytest.mark.parametrize("fn", [adaptive.swap_row, mo.swap_row], ids=["product", "oracle"])
+@pytest.mark.parametrize("case", range(len(_REF_SWAP_CASES)))
+def test_reference_swap_row_known_answers(fn, case):
+    experts, weights, keep, held, eps, want, weight_at = _REF_SWAP_CASES[case]
+    got_e, got_w = fn(list(experts), list(weights), keep, held.__contains__, eps)
+    assert got_e == want
+    for pos, w in weight_at.items():
+        assert got_w[pos] == pytest.approx(w)
+    # a weight follows its expert (:74-79)
+    pairs = dict(zip(got_e, got_w))
+    for e, w in zip(experts, weights):
+        assert pairs[e] == pytest.approx(w)
+
+
+def test_reference_swap_row_set_and_identity_rules():
+    """test_swap_routing.py:38-57,66-72: unchanged rows are the input list
+    itself (product), one spare serves one pick, and the expert and weight
+    multisets are preserved."""
+    before = [1, 7, 9]
+    e, _ = adaptive.swap_row(before, [0.5, 0.021, 0.019], 2, {1, 7, 9}.__contains__, 0.02)
+    assert e is before
+    e, _ = adaptive.swap_row(before, [0.5, 0.021, 0.019], 2, {1}.__contains__, 0.02)
+    assert e is before
+    for fn in (adaptive.swap_row, mo.swap_row):
+        e, _ = fn([7, 8, 9], [0.021, 0.020, 0.019], 2, {9}.__contains__, 0.02)
+        assert e.count(9) == 1 and sorted(e) == [7, 8, 9]
+        e, w = fn([1, 7, 9, 10], [0.5, 0.021, 0.020, 0.019], 2, {9, 10}.__contains__, 0.02)
+        assert sorted(e) == [1, 7, 9, 10]
+        assert sorted(round(v, 6) for v in w) == sorted(round(v, 6) for v in [0.5, 0.021, 0.020, 0.019])
+
+
+@pytest.mark.parametrize("fn", ["product", "oracle"])
+def test_blend_is_a_bf16_scalar(fn):
+    """Renorm blend 0.3 rounds to bf16 0.30078125 before it multiplies
+    (compiled.py:111 builds mx.array(blend, scores.dtype)).  Row gates
+    [0.5, 0.2734375, 0.2265625] at threshold 0.7 keep two slots: topk mass 1,
+    kept mass 0.7734375, diff -0.2265625.  By hand: 0.30078125 * -0.2265625 =
+    -0.068145751953125 -> bf16 -0.068359375; 1 - 0.068359375 = 0.931640625,
+    a tie between 0.9296875 and 0.93359375 -> the even 0.9296875.  Scores:
+    0.5 / 0.9296875 = 0.53782 -> 0.5390625, 0.2734375 / 0.9296875 = 0.29412 ->
+    0.294921875.  With blend left in fp32 the normalizer would be 0.93359375
+    and the first score 0.53515625."""
+    inds = np.array([[4, 9, 2]], np.int32)
+    gates = np.array([[0.5, 0.2734375, 0.2265625]], np.float32)
+    adaptive.set_threshold(0.7)
+    if fn == "product":
+        _, scores, keeps, width = adaptive.plan(3, inds, gates, 0.3)
+        assert keeps == [2] and width == 2
+    else:
+        _, scores, keeps = mo.adaptive_routes(inds, gates, 0.7, "bf16", blend=0.3)
+    np.testing.assert_array_equal(np.asarray(scores)[0, :2], np.array([0.5390625, 0.294921875], np.float32))
+
+
+def test_keep_stats_count_exact_layers():
+    """Layers at threshold 1.0 record k per row too (adaptive_topk.py:236-239),
+    so the keep statistics mix exact and adaptive layers as the reference's do."""
+    adaptive.set_layer_thresholds({1: 0.5})
+    adaptive.record_exact(0, rows=3, k=4)
+    assert adaptive.last_keeps()[0] == (4, 4, 4)
+    rng = np.random.default_rng(19)
+    inds, g = _rows(rng, 2, 4, 16)
+    _, _, keeps, _ = adaptive.plan(1, inds, g)
+    assert adaptive.last_keeps()[1] == tuple(keeps)
+    assert adaptive.mean_keeps() == pytest.approx((12 + sum(keeps)) / 5)
+    adaptive.record_exact(None, rows=3, k=4)   # no layer id: nothing
+    assert adaptive.mean_keeps() == pytest.approx((12 + sum(keeps)) / 5)

@@ -31,18 +31,23 @@ def _near_tie(gates_row, k):
     return order[k - 1] - order[k] <= 1
 
 
-@pytest.mark.parametrize("tokens", [1, 6, 40, 130], ids=["decode-1", "decode-6", "rows-40", "grouped-130"])
-def test_adaptive_layer_against_the_oracle(device, tokens):
+@pytest.mark.parametrize("tokens,blend", [(1, 1.0), (6, 1.0), (40, 1.0), (130, 1.0), (6, 0.3), (130, 0.3)],
+                         ids=["decode-1", "decode-6", "rows-40", "grouped-130", "decode-6-blend0.3",
+                              "grouped-130-blend0.3"])
+def test_adaptive_layer_against_the_oracle(device, tokens, blend):
+    """Blend 0.3 (FLASHNEXT_RENORM_BLEND) renormalises over a mix of the kept
+    and the top-k mass, with blend rounded to bf16 as the reference does."""
     seed = 410 + tokens
     adaptive.set_threshold(0.6)
     adaptive.set_min_keep(2)
     layer = assemble.build_layer(SPEC, seed, device, dense=True)
+    layer.renorm_blend = blend
     x_np = mo.bf16_bits_to_f32(synth.tokens(SPEC, seed, tokens))
     y = host(layer(bf16_device(x_np, device)))
     torch.cuda.synchronize()
     path = "decode" if tokens <= 8 else "prefill"
     ref = mo.moe_layer(x_np, synth.numpy_layer(SPEC, seed), "bf16", path=path,
-                       adaptive=dict(threshold=0.6, min_keep=2))
+                       adaptive=dict(threshold=0.6, min_keep=2, blend=blend))
     width = ref["inds"].shape[1]
     inds = layer.last_inds.cpu().numpy()
     same = (inds[:, :width] == ref["inds"]).all(axis=1)

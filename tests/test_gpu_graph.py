@@ -62,3 +62,52 @@ def test_step_graph_refuses_host_lru_layers_and_detached_state(device):
     pool.detach_device_lru()
     with pytest.raises(RuntimeError):
         graph.replay()
+
+
+def test_step_graph_survives_a_grouped_call_and_refuses_adaptive_routing(device):
+    """A call above the decode bound hands the LRU state to the host and
+    uploads it back into the same device buffers, so a graph recorded before
+    it replays on: equal to an eager twin that ran the same calls, and to the
+    dense layers.  With a threshold below 1.0 (or a route observer) a graph
+    would route exactly where the eager call adapts: replay and build raise."""
+    from veymoe import adaptive
+
+    layers, slots = 2, 40
+    store_a, pool_a, pooled_a, dense = pooled_stack(device, SMALL, layers, slots, SEED)
+    store_b, pool_b, pooled_b, _ = pooled_stack(device, SMALL, layers, slots, SEED)
+    lru_a = pool_a.attach_device_lru(store_a)
+    lru_b = pool_b.attach_device_lru(store_b)
+    graph = StepGraph(pooled_a, device=device).capture()
+    eager = StepGraph(pooled_b, device=device)
+    for step in range(4):
+        if step == 2:   # a 12-row call on layer 0 of both stacks
+            xg = assemble.tokens_tensor(SMALL, SEED, device, 12, stream=77)
+            ga, gb = pooled_a[0](xg[None]), pooled_b[0](xg[None])
+            assert torch.equal(ga.view(torch.int16), gb.view(torch.int16))
+            assert pool_a.device_lru is lru_a and pool_b.device_lru is lru_b
+        x = _inputs(SMALL, layers, 1, step, device)
+        got = graph.replay(x).clone()
+        eager.x.copy_(x)
+        want = eager.run_eager().clone()
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), step
+        for l in range(layers):
+            ref = dense[l](x[l][None])[0]
+            assert torch.equal(got[l].view(torch.int16), ref.view(torch.int16)), (step, l)
+        for a, b in zip(lru_a.state(), lru_b.state()):
+            assert (a == b).all(), step
+    try:
+        adaptive.set_layer_thresholds({1: 0.5})
+        with pytest.raises(RuntimeError):
+            graph.replay()
+        with pytest.raises(RuntimeError):
+            StepGraph(pooled_a, device=device)
+        adaptive.set_layer_thresholds()
+        adaptive.set_route_observer(lambda *a: None)
+        with pytest.raises(RuntimeError):
+            graph.replay()
+    finally:
+        adaptive.set_layer_thresholds()
+        adaptive.set_route_observer()
+    graph.replay()
+    torch.cuda.synchronize()

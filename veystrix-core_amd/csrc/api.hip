@@ -431,7 +431,9 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   w.words = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
   w.fill = w.words + align_up(uint64_t(T) * K * 4);
   w.tags = w.fill + align_up(4 + 8 * uint64_t(vm::kLruMaxRouted));
-  w.total = w.tags + align_up(vm::tag_words(K * I) * 4);   // hand-off words of the one-token pipeline
+  // hand-off words of the two-launch one-token pipeline: one-token bf16 calls
+  // are the only ones it takes
+  w.total = w.tags + (T == 1 && dtype == VM_BF16 ? align_up(vm::tag_words(K * I) * 4) : 0);
   return w;
 }
 

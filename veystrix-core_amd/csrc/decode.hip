@@ -6,15 +6,17 @@
 //
 //   k_front   router logits x . Wr^T (one row per wave, bf16 dot2) and the
 //             shared expert's H -> 1 Q4 gate with its sigmoid.
-//   k_gateup  in every block of a routed pair, every wave recomputes the
-//             token's softmax from the logits and finds the expert of its
-//             slot's rank (ballot search + candidate ranking, no sort) and maps
-//             it to its slot: no barrier stands before the weight loads.
-//             Every lane then streams gate and up Q4/G32 rows against its
-//             activation groups held in registers; SwiGLU runs on the lanes
-//             that hold the row sums.  Shared-expert pairs skip the selection.
-//             One block per token publishes the ordered selection (indices,
-//             scores, route words) for k_down.
+//   k_gateup  in every block of a routed pair, one chooser wave recomputes
+//             the token's softmax from the logits, extracts the key of its
+//             slot's rank from the lanes' sorted keys by wave maxima
+//             (vm_select.h), maps the expert to its slot through the slot
+//             table entries it loaded beside the logits, and hands the route
+//             word to the block's other wave through LDS.  Every lane then
+//             streams gate and up Q4/G32 rows against its activation groups
+//             held in registers; SwiGLU runs on the lanes that hold the row
+//             sums.  Shared-expert pairs skip the selection.  One block per
+//             token publishes the ordered selection (indices, scores, route
+//             words) for k_down.
 //   k_down    down Q4/G32 GEMV of every slot of a token for a tile of output
 //             rows (one slot per wave), then the router-score
 //             combine with the shared term after one barrier.

@@ -404,7 +404,8 @@ __device__ typename Cand<A>::T rank_order(const GateKeys<A>& g, uint32_t K, uint
 
 // Renormalised score of lane k's candidate `top` (rank order in cand[0..K)):
 // gate / (mass + blend*(selected_mass - mass)), each step rounded to the
-// activation type; the mass is summed in rank order.
+// activation type, blend included (the reference multiplies by blend as a
+// scalar of the scores' type); the mass is summed in rank order.
 template <class A>
 __device__ float score_of_order(const typename Cand<A>::T* cand, typename Cand<A>::T top, uint32_t K, float blend,
                                 uint32_t lane) {
@@ -412,7 +413,7 @@ __device__ float score_of_order(const typename Cand<A>::T* cand, typename Cand<A
   for (uint32_t i = 0; i < K; ++i) mass += GateKeys<A>::gate(Cand<A>::key(cand[i]));
   mass = A::round(mass);
   const float diff = A::round(mass - mass);
-  const float normalizer = A::round(mass + A::round(blend * diff));
+  const float normalizer = A::round(mass + A::round(A::round(blend) * diff));
   return lane < K ? A::round(GateKeys<A>::gate(Cand<A>::key(top)) / normalizer) : 0.0f;
 }
 

@@ -105,6 +105,17 @@ def observe_exact(layer: Optional[int], inds: np.ndarray, gates: np.ndarray) -> 
     _observer(layer, np.asarray(inds)[:n].tolist(), np.asarray(gates)[:n].tolist(), [k] * n)
 
 
+def record_exact(layer: Optional[int], rows: int, k: int) -> None:
+    """A call at threshold 1.0 keeps all k slots of every row; the keep
+    statistics count it (adaptive_topk.py:236-239)."""
+    global _keep_sum, _keep_count
+    if layer is None:
+        return
+    _last_keeps[layer] = (k,) * rows
+    _keep_sum += rows * k
+    _keep_count += rows
+
+
 def last_keeps() -> Dict[int, Tuple[int, ...]]:
     return dict(_last_keeps)
 
@@ -209,6 +220,7 @@ def plan(layer: Optional[int], inds: np.ndarray, gates: np.ndarray, blend: float
     topk_mass = rnd(gates.astype(np.float64).sum(axis=1, keepdims=True))
     kept_mass = rnd(kept.astype(np.float64).sum(axis=1, keepdims=True))
     diff = rnd(kept_mass - topk_mass)
-    normalizer = rnd(topk_mass + rnd(np.float32(blend) * diff))
+    # blend is a scalar of the scores' type (compiled.py:111)
+    normalizer = rnd(topk_mass + rnd(rnd(np.float32(blend)) * diff))
     scores = rnd(kept.astype(np.float64) / normalizer.astype(np.float64))
     return out_inds, scores, effective, width

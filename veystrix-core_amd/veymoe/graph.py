@@ -13,7 +13,10 @@ every layer for the step), ``out``, ``inds`` and ``scores``.  ``replay(x)``
 copies the step's inputs in and launches the graph; the device LRU state moves
 on exactly as with eager calls.  Layers whose pool would need the host LRU
 (partly resident, no device LRU) are refused, and so is a replay after a
-pool's device LRU was detached (its buffers are gone).
+pool's device LRU was detached and not attached again over the same buffers.
+A graph records exact top-k routing, so building or replaying one while
+adaptive routing (a threshold below 1.0) or a route observer is active for
+any of its layers raises: the eager layer call would route differently.
 """
 from __future__ import annotations
 
@@ -22,9 +25,17 @@ from typing import Sequence
 
 import torch
 
-from . import _lib
+from . import _lib, adaptive
 from .device import stream_handle
 from .layer import MAX_DECODE_ROWS, MoELayer
+
+
+def _refuse_adaptive(layers) -> None:
+    if adaptive.observing():
+        raise RuntimeError("a step graph records exact routing: clear the route observer first")
+    for i, layer in enumerate(layers):
+        if adaptive.threshold_for(layer._flashnext_layer_id) < 1.0:
+            raise RuntimeError(f"a step graph records exact routing: layer {i} has an adaptive threshold below 1.0")
 
 
 def _device_only(layer: MoELayer) -> bool:
@@ -41,6 +52,7 @@ class StepGraph:
             raise ValueError("a step needs at least one layer")
         if not 1 <= rows <= MAX_DECODE_ROWS:
             raise ValueError(f"a captured step serves 1..{MAX_DECODE_ROWS} rows")
+        _refuse_adaptive(layers)
         for i, layer in enumerate(layers):
             if not _device_only(layer):
                 raise ValueError(f"layer {i} needs the host LRU (attach a device LRU to its pool)")
@@ -74,6 +86,7 @@ class StepGraph:
         self.graph = None
 
     def _check_state(self) -> None:
+        _refuse_adaptive(self.layers)
         for pool, lru in self._lrus:
             if pool.device_lru is not lru:
                 raise RuntimeError("a pool's device LRU was detached since the step was built")

@@ -288,24 +288,37 @@ class MoELayer:
         self._set_inject(args, flat, inject)
         lib = _lib.lib()
         sw = self.switch_mlp
+        layer = self._flashnext_layer_id
+        exact = adaptive.threshold_for(layer) >= 1.0
+        if exact:
+            adaptive.record_exact(layer, tokens, self.top_k)
         lru = sw.pool.device_lru if sw.pool is not None else None
         if lru is not None:
-            if tokens > MAX_DECODE_ROWS or adaptive.threshold_for(self._flashnext_layer_id) < 1.0 or \
-                    adaptive.observing():
+            if tokens > MAX_DECODE_ROWS or not exact or adaptive.observing():
                 # the grouped path and the adaptive plan resolve their
-                # experts on the host: hand the LRU state back for this call
+                # experts on the host: hand the LRU state back for this call,
+                # then upload it into the same device buffers (a sync and an
+                # O(slots) host pass each way)
                 sw.pool.detach_device_lru()
                 try:
-                    return self.forward(flat, inject)
+                    return self._forward_host(args, inds, scores, flat, out, exact)
                 finally:
-                    sw.pool.attach_device_lru(lru.store)
+                    sw.pool.attach_device_lru(lru.store, reuse=lru)
             if tokens * self.top_k > lru.usable_slots:
                 raise ValueError("requested experts exceed expert pool capacity")
             # router, assign, fill and experts on the device: no route sync
             _lib.check(lib.vm_moe_layer_lru(args, lru.view(sw.layer_id), stream_handle()))
             self.last_inds, self.last_scores = inds, scores
             return out
-        if adaptive.threshold_for(self._flashnext_layer_id) < 1.0 or adaptive.observing():
+        return self._forward_host(args, inds, scores, flat, out, exact)
+
+    def _forward_host(self, args, inds: torch.Tensor, scores: torch.Tensor, flat: torch.Tensor, out: torch.Tensor,
+                      exact: bool) -> torch.Tensor:
+        """The layer call whose routes the host may see: the adaptive plan or
+        a route observer, or a pool whose LRU state is on the host."""
+        lib = _lib.lib()
+        sw = self.switch_mlp
+        if not exact or adaptive.observing():
             return self._forward_adaptive(args, inds, scores, flat, out)
         if sw.pool is not None and not sw._pool_fully_resident():
             # router, then the host LRU pass on synced routes, then the experts

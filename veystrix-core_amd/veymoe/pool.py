@@ -300,13 +300,18 @@ class ExpertPool:
 
 
     # ------------------------------------------------------ device LRU ---
-    def attach_device_lru(self, source: HostRecordStore) -> "DeviceLru":
+    def attach_device_lru(self, source: HostRecordStore, reuse: "DeviceLru" = None) -> "DeviceLru":
         """Move the LRU state to the device; misses are then filled from
         ``source`` by the GPU itself.  Host-side LRU calls raise until
-        ``detach_device_lru``."""
+        ``detach_device_lru``.  ``reuse``: a device LRU this pool detached
+        earlier; its buffers take the current state, so step graphs recorded
+        over them stay valid (a new one is made if the queue length changed)."""
         if self.device_lru is not None:
             raise RuntimeError("a device LRU is already attached")
-        self.device_lru = DeviceLru(self, source)
+        if reuse is not None and reuse.pool is self and reuse.store is source and reuse.reload():
+            self.device_lru = reuse
+        else:
+            self.device_lru = DeviceLru(self, source)
         return self.device_lru
 
     def detach_device_lru(self) -> None:
@@ -384,6 +389,20 @@ class DeviceLru:
                 host_row[layer, expert] = row
         self.host_row = torch.from_numpy(host_row).to(dev)
         self._views = {}
+
+    def reload(self) -> bool:
+        """Upload the pool's host LRU state into these buffers (same device
+        addresses) and zero the counters, whose counts the detach folded into
+        the pool.  False when the queue length changed (a slot was discarded)."""
+        pool = self.pool
+        pool.sync_tables()
+        owner, order = order_state(pool)
+        if len(order) != self.order_len:
+            return False
+        self.slot_owner.copy_(torch.from_numpy(owner))
+        self.lru_order.copy_(torch.from_numpy(order))
+        self.counters.zero_()
+        return True
 
     def view(self, layer: int) -> _lib.VmDeviceLru:
         v = self._views.get(layer)
