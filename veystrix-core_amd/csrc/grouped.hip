@@ -12,14 +12,15 @@
 //            features).  Workgroups are dealt to the eight XCDs round-robin;
 //            each XCD takes a contiguous run of the sorted tiles with all their
 //            slices, so the slices of one row tile share its L2 copy of the
-//            tile's A rows and the tiles of one expert share its weights.  K runs in chunks of
-//            eight 32-input groups.  Per chunk the block stages in LDS (one
-//            stage for the Q4 GEMMs, two for the router): the A rows (32
-//            lanes per 512-byte row segment,
-//            pair-permuted to match the dequantised weights), the Q4 weight
-//            row chunks (8 lanes per 128-byte line) and the scale and bias
-//            vectors; the 16-byte units of A rows and weight lines are
-//            XOR-swizzled so the MFMA lanes' LDS reads are conflict-free.  Each lane dequantises its 16-byte Q4 groups into bf16
+//            tile's A rows and the tiles of one expert share its weights.
+//            K runs in chunks of eight 32-input groups.  Per chunk the block
+//            stages in LDS (one stage for the Q4 GEMMs, two for the router):
+//            the A rows (32 lanes per 512-byte row segment, in input order),
+//            the Q4 weight row chunks (8 lanes per 128-byte line) and the
+//            scale and bias vectors; the 16-byte units of A rows and weight
+//            lines are XOR-swizzled so the MFMA lanes' LDS reads are
+//            conflict-free.  Each lane dequantises its 16-byte Q4 groups into
+//            bf16 in input order
 //            (f16 magic number + v_fma_mix + v_cvt_pk_bf16_f32) and feeds
 //            v_mfma_f32_16x16x32_bf16 with fp32 accumulation.  The MFMA loop
 //            is specialised on the number of 16-row blocks in use, so it has
@@ -140,11 +141,21 @@ __device__ __forceinline__ uint32_t f16_magic() {
   return m;
 }
 
-// 8 inputs of one packed word -> bf16 pairs (q_n, q_{n+4}) for n < 4, the
-// order pair_activations gives the activations.  (1024 + q) and (1024 + 16 q)
-// are exact in f16, so w = s*q + b is one fp32 fma per value:
-// s*(1024 + q) + (b - 1024 s) for the low nibble of a byte and
-// (s/16)*(1024 + 16 q) + (b - 64 s) for the high one.
+// Operand order of the MFMA k slots: 1 = input order (the activation rows
+// are used as loaded and the dequantised pairs are packed (q_0 q_1) .. (q_6
+// q_7)); 0 = pair-permuted ((q_n q_{n+4}) pairs, with every activation unit
+// permuted the same way when it is staged).  Both feed each k slot the same
+// product; the MFMA's sum does not depend on the slot order (the two give the
+// same bits).
+#ifndef VM_DQ_NATURAL
+#define VM_DQ_NATURAL 1
+#endif
+constexpr bool kNatural = VM_DQ_NATURAL;
+
+// 8 inputs of one packed word -> 4 bf16 pairs in the operand order above.
+// (1024 + q) and (1024 + 16 q) are exact in f16, so w = s*q + b is one fp32
+// fma per value: s*(1024 + q) + (b - 1024 s) for the low nibble of a byte
+// and (s/16)*(1024 + 16 q) + (b - 64 s) for the high one.
 struct Dequant {
   float s, b1024, s16, b64;
   __device__ __forceinline__ Dequant(float scale, float b) {
@@ -157,21 +168,40 @@ struct Dequant {
     const uint32_t w8 = w >> 8;
     const uint32_t m[4] = {(w & 0x000F000Fu) | magic, (w & 0x00F000F0u) | magic, (w8 & 0x000F000Fu) | magic,
                            (w8 & 0x00F000F0u) | magic};
+    float lo[4], hi[4];  // q_n and q_{n+4}, n < 4
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
       const f16x2_t h = __builtin_bit_cast(f16x2_t, m[n]);
       const float sc = n & 1 ? s16 : s, bc = n & 1 ? b64 : b1024;
-      out[n] = pack_bf16(fmaf(sc, static_cast<float>(h.x), bc), fmaf(sc, static_cast<float>(h.y), bc));
+      lo[n] = fmaf(sc, static_cast<float>(h.x), bc);
+      hi[n] = fmaf(sc, static_cast<float>(h.y), bc);
+    }
+    if constexpr (kNatural) {
+      out[0] = pack_bf16(lo[0], lo[1]);
+      out[1] = pack_bf16(lo[2], lo[3]);
+      out[2] = pack_bf16(hi[0], hi[1]);
+      out[3] = pack_bf16(hi[2], hi[3]);
+    } else {
+#pragma unroll
+      for (int n = 0; n < 4; ++n) out[n] = pack_bf16(lo[n], hi[n]);
     }
   }
 };
 
-// bf16 weights: natural pairs (k0 k1)(k2 k3)(k4 k5)(k6 k7) -> (k0 k4)(k1 k5)(k2 k6)(k3 k7)
+// bf16 weights in the operand order: as loaded, or natural pairs (k0 k1)(k2
+// k3)(k4 k5)(k6 k7) -> (k0 k4)(k1 k5)(k2 k6)(k3 k7)
 __device__ __forceinline__ void permute_word(const uint4 v, uint32_t out[4]) {
-  out[0] = (v.x & 0xffffu) | (v.z << 16);
-  out[1] = (v.x >> 16) | (v.z & 0xffff0000u);
-  out[2] = (v.y & 0xffffu) | (v.w << 16);
-  out[3] = (v.y >> 16) | (v.w & 0xffff0000u);
+  if constexpr (kNatural) {
+    out[0] = v.x;
+    out[1] = v.y;
+    out[2] = v.z;
+    out[3] = v.w;
+  } else {
+    out[0] = (v.x & 0xffffu) | (v.z << 16);
+    out[1] = (v.x >> 16) | (v.z & 0xffff0000u);
+    out[2] = (v.y & 0xffffu) | (v.w << 16);
+    out[3] = (v.y >> 16) | (v.w & 0xffff0000u);
+  }
 }
 
 __device__ __forceinline__ bf16x8_t as_operand(const uint32_t r[4]) {
@@ -420,7 +450,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
 #pragma unroll
     for (int j = 0; j < kItems; ++j) {
       if (!kAllItems && tid + j * kThreads >= static_cast<uint32_t>(kItemsAll)) continue;
-      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + a_off(j)) = pair_perm(ar[j]);
+      *reinterpret_cast<uint4*>(s_a0 + buf * kStage + a_off(j)) = kNatural ? ar[j] : pair_perm(ar[j]);
     }
 #pragma unroll
     for (int j = 0; j < kSItems; ++j) {
@@ -925,8 +955,9 @@ __device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item,
       const uint32_t it = j * kThreads + tid;
       const uint32_t r = it / kUnits, u = it % kUnits;
       const uint4 x = av[j];
-      const uint4 pp = make_uint4((x.x & 0xffffu) | (x.z << 16), (x.x >> 16) | (x.z & 0xffff0000u),
-                                  (x.y & 0xffffu) | (x.w << 16), (x.y >> 16) | (x.w & 0xffff0000u));
+      const uint4 pp = kNatural ? x
+                                : make_uint4((x.x & 0xffffu) | (x.z << 16), (x.x >> 16) | (x.z & 0xffff0000u),
+                                             (x.y & 0xffffu) | (x.w << 16), (x.y >> 16) | (x.w & 0xffff0000u));
       const uint32_t phys = (u & ~15u) | ((u ^ rows_swz(r, u / (kQG * 4))) & 15u);
       *reinterpret_cast<uint4*>(s_a + r * kRowBytes + phys * 16u) = pp;
     }
@@ -1435,6 +1466,10 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
   // a call with no routed experts is the shared expert's own GEMM (run on a
   // side stream beside the routing), timed apart from the routed experts
   const bool own = p.experts == 0;
+  // tiles of up to 64 rows (every instance here) take the DMA-ring kernel
+  // where its shapes fit and it is selected
+  if (epi != kEpiLogits && qring_mode(-1) == 1 && qring_supported(epi, p.k_dim, p.n_dim))
+    return launch_qring(epi, p, max_tiles, stream);
   switch (epi) {
     case kEpiSwiglu:
       return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>(own ? "shared_gateup" : "grouped_gateup", p,
