@@ -424,17 +424,6 @@ int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride,
  * tests of the pipelines. */
 int vm_decode_pipeline(int mode);
 
-/* vm_grouped_ring: the Q4 GEMMs (gate/up + SwiGLU, down) of calls above 64
- * rows, process-wide:
- *   1 (the default): every operand streamed global -> LDS through a DMA ring
- *     (K of 512, 1024, 2048 or 4096; other K take the chunked GEMM);
- *   0: the chunked GEMM (operands staged through registers, one chunk ahead).
- * Both compute the matrix form of the reference's gather_qmm (weights rounded
- * to bf16, fp32 sums) in different fp32 orders.  -1 queries.  Returns the
- * previous setting.  No counterpart in the reference: it is for A/B
- * measurement and the parity tests of both kernels. */
-int vm_grouped_ring(int mode);
-
 /* Per-kernel event timing over a window of calls (for rooflines).  While
  * enabled, every kernel the library launches is bracketed by hipEvents on its
  * stream; vm_timing_read returns the summed milliseconds and launch count of

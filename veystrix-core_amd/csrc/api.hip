@@ -1444,11 +1444,6 @@ int vm_decode_pipeline(int mode) {
   return g_fused_decode.exchange(mode);
 }
 
-int vm_grouped_ring(int mode) {
-  if (mode < -1 || mode > 1) return fail(VM_EINVAL, "mode must be -1 (query), 0 or 1");
-  return vm::qring_mode(mode);
-}
-
 int vm_timing_enable(int enabled) {
   Timing& t = timing();
   std::lock_guard<std::mutex> lock(t.mu);

@@ -1466,10 +1466,6 @@ hipError_t launch_grouped(int epi, const GroupedLaunch& p, uint32_t max_tiles, h
   // a call with no routed experts is the shared expert's own GEMM (run on a
   // side stream beside the routing), timed apart from the routed experts
   const bool own = p.experts == 0;
-  // tiles of up to 64 rows (every instance here) take the DMA-ring kernel
-  // where its shapes fit and it is selected
-  if (epi != kEpiLogits && qring_mode(-1) == 1 && qring_supported(epi, p.k_dim, p.n_dim))
-    return launch_qring(epi, p, max_tiles, stream);
   switch (epi) {
     case kEpiSwiglu:
       return grouped_go<kEpiSwiglu, VM_GU_WAVES, VM_GU_NBW, 2>(own ? "shared_gateup" : "grouped_gateup", p,

@@ -247,15 +247,6 @@ struct GroupedLaunch {
 bool router_gemm_supported(uint32_t k_dim, uint32_t n_dim);
 hipError_t launch_router_gemm(const GroupedLaunch& p, hipStream_t stream);
 
-// The Q4 gate/up (kEpiSwiglu) and down (kEpiRows) GEMMs of calls above 64
-// rows with every operand streamed global -> LDS through a DMA ring
-// (qring.hip): K of 512, 1024, 2048 or 4096, n_dim a multiple of 64, tiles
-// of at most 64 rows.  qring_mode(-1) queries the process-wide choice (1: the
-// ring, 0: the chunked GEMM), qring_mode(m) sets it and returns the previous.
-int qring_mode(int mode);
-bool qring_supported(int epi, uint32_t k_dim, uint32_t n_dim);
-hipError_t launch_qring(int epi, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream);
-
 struct SortLaunch {
   const int32_t* inds;         // [tokens, slots]
   uint32_t* row_off;           // [groups + 1]

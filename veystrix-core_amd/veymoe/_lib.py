@@ -198,7 +198,6 @@ SIGNATURES = {
                                      ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64),
                                      _c_u32, _vp]),
     "vm_decode_pipeline": (ctypes.c_int, [ctypes.c_int]),
-    "vm_grouped_ring": (ctypes.c_int, [ctypes.c_int]),
     "vm_timing_enable": (ctypes.c_int, [ctypes.c_int]),
     "vm_timing_read": (ctypes.c_int, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_uint64)]),
