@@ -722,7 +722,7 @@ def main():
     parser.add_argument("--pipeline", type=int, default=0, choices=(0, 1, 2),
                         help="one-token decode kernels (vm_decode_pipeline): 0 router, gate/up, down (default); "
                              "1 front with the shared expert + gate/up grid + down; 2 front + experts grid with "
-                             "the tagged hand-off")
+                             "the tagged hand-off (1 and 2 need a library built with -DVM_FUSED_PIPELINES=1)")
     parser.add_argument("--cpu-seconds", type=float, default=12.0)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-grouped", action="store_true",
@@ -757,7 +757,8 @@ def main():
     spec = synth.CONFIGS["decode"]
     layers = args.layers
     from veymoe import _lib
-    _lib.lib().vm_decode_pipeline(args.pipeline)
+    if _lib.lib().vm_decode_pipeline(args.pipeline) < 0:
+        sys.exit(f"bench.py: --pipeline {args.pipeline}: {_lib.last_error()}")
     timing, stack, pool, graph = run_decode(spec, layers, args.steps, args.warmup, args.seed, args.eager)
     kernels, nbytes = timing["kernels"], timing["bytes"]
     layer_s = timing["layer_s"]

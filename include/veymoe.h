@@ -420,8 +420,10 @@ int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride,
  *   2: two launches, the front and one experts grid that hands its gate/up
  *     activations to its down rows through tagged words.
  * All three give the same bits.  -1 queries.  Returns the previous setting.
- * No counterpart in the reference: it is for A/B measurement and the parity
- * tests of the pipelines. */
+ * Pipelines 1 and 2 were measured slower than 0 and are compiled only into a
+ * library built with -DVM_FUSED_PIPELINES=1; otherwise modes 1 and 2 return
+ * VM_EUNSUPPORTED.  No counterpart in the reference: it is for A/B
+ * measurement and the parity tests of the pipelines. */
 int vm_decode_pipeline(int mode);
 
 /* Per-kernel event timing over a window of calls (for rooflines).  While

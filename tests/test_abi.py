@@ -240,8 +240,25 @@ def test_decode_workspace_reserves_hand_off_words_for_one_token_bf16_only():
     per = lib.vm_moe_layer_workspace(8, 10, 2048, 512, 512, 512, 1)
     assert per == 199424
     assert lib.vm_moe_layer_workspace(2048, 10, 2048, 512, 512, 512, 1) == 256 * 199424
-    # one bf16 token: its own sizes plus the pipeline's tag words (one 32-bit
-    # word per activation of the ten routed slots at least)
+    # one token: fp32 by the same hand layout (logits 2048, activations
+    # 22528, the rest 256 each, fill list 768) is 26624 B; bf16 (activations
+    # 11264) 15360 B, plus the two-launch pipeline's hand-off words (at least
+    # one 32-bit word per routed activation) when the library carries it
+    assert lib.vm_moe_layer_workspace(1, 10, 2048, 512, 512, 512, 1) == 26624
     one = lib.vm_moe_layer_workspace(1, 10, 2048, 512, 512, 512, 0)
-    one_f32 = lib.vm_moe_layer_workspace(1, 10, 2048, 512, 512, 512, 1)
-    assert one - one_f32 >= 10 * 512 * 4 - 11 * 512 * 2
+    if _lib.lib_built_with_fused_pipelines():
+        assert one >= 15360 + 10 * 512 * 4
+    else:
+        assert one == 15360
+
+
+def test_default_build_carries_the_default_pipeline_only():
+    """The one-token pipelines 1 and 2 (measured slower) are compiled only
+    with -DVM_FUSED_PIPELINES=1; the shipped build refuses them."""
+    lib = _lib.lib()
+    if _lib.lib_built_with_fused_pipelines():
+        pytest.skip("this library was built with the one-token pipelines")
+    assert lib.vm_decode_pipeline(-1) == 0
+    assert lib.vm_decode_pipeline(1) == _lib.VM_EUNSUPPORTED
+    assert "VM_FUSED_PIPELINES" in _lib.last_error()
+    assert lib.vm_decode_pipeline(0) == 0

@@ -431,9 +431,9 @@ static LayerWs layer_ws(uint32_t T, uint32_t K, uint32_t I, uint32_t Is, uint32_
   w.words = w.scores + align_up(uint64_t(T) * K * act_bytes(dtype));
   w.fill = w.words + align_up(uint64_t(T) * K * 4);
   w.tags = w.fill + align_up(4 + 8 * uint64_t(vm::kLruMaxRouted));
-  // hand-off words of the two-launch one-token pipeline: one-token bf16 calls
-  // are the only ones it takes
-  w.total = w.tags + (T == 1 && dtype == VM_BF16 ? align_up(vm::tag_words(K * I) * 4) : 0);
+  // hand-off words of the two-launch one-token pipeline (built on request):
+  // one-token bf16 calls are the only ones it takes
+  w.total = w.tags + (VM_FUSED_PIPELINES && T == 1 && dtype == VM_BF16 ? align_up(vm::tag_words(K * I) * 4) : 0);
   return w;
 }
 
@@ -1440,6 +1440,8 @@ int vm_pool_stage(void* pool_base, uint64_t header_size, uint64_t record_stride,
 
 int vm_decode_pipeline(int mode) {
   if (mode < -1 || mode > 2) return fail(VM_EINVAL, "mode must be -1 (query) or 0..2");
+  if (!VM_FUSED_PIPELINES && mode > 0)
+    return fail(VM_EUNSUPPORTED, "pipelines 1 and 2 are built only with -DVM_FUSED_PIPELINES=1");
   if (mode == -1) return g_fused_decode.load();
   return g_fused_decode.exchange(mode);
 }

@@ -97,6 +97,10 @@ struct DownLaunch {
 };
 
 // ---------------------------------------------------- fused decode (T = 1) --
+// The one-token pipelines are built only on request (A/B measurement).
+#ifndef VM_FUSED_PIPELINES
+#define VM_FUSED_PIPELINES 0
+#endif
 // A decode call of one token (fused.hip): the front (router logits, the
 // shared expert's gate/up + SwiGLU and its sigmoid gate) and one grid of a
 // block per CU for the routed experts: either gate/up only, followed by the

@@ -253,3 +253,17 @@ def check(code: int) -> None:
         if code == VM_EINVAL:
             raise ValueError(message)
         raise VeymoeError(code, message)
+
+
+def lib_built_with_fused_pipelines():
+    """Whether the built library carries the one-token pipelines 1 and 2 (a
+    library built with -DVM_FUSED_PIPELINES=1); None when it is not built."""
+    if not os.path.exists(LIB_PATH):
+        return None
+    handle = lib()
+    previous = handle.vm_decode_pipeline(-1)
+    rc = handle.vm_decode_pipeline(1)
+    if rc < 0:
+        return False
+    handle.vm_decode_pipeline(previous)
+    return True
