@@ -470,7 +470,10 @@ struct RouterChunk<ActF32> {
 // Tokens per row of router blocks (grid y), and tokens whose activations a
 // router wave loads together before their dot products.
 constexpr uint32_t kFrontTokens = 8;
-constexpr int kFrontUnroll = 4;
+#ifndef VM_FRONT_UNROLL
+#define VM_FRONT_UNROLL 4
+#endif
+constexpr int kFrontUnroll = VM_FRONT_UNROLL;
 
 // One router row per wave over tokens [t_begin, t_end).  CH = 16-byte chunks
 // per lane per row (hidden/512, rounded up).  U tokens at a time: their loads
