@@ -1,0 +1,61 @@
+"""Register budgets of the chunked grouped GEMMs, from the compiler's
+resource report (no GPU needed).
+
+The occupancy these kernels are tuned for is set by their registers as much
+as by their LDS:
+* the down GEMM (`k_grouped<1, 8, 2, 1, false, *>`) runs two 8-wave blocks per
+  CU, four waves per SIMD, so its VGPRs + AGPRs must stay at or below 128 of
+  the SIMD's 512 per lane;
+* the gate/up GEMM (`k_grouped<0, 4, 1, 2, false, *>`) runs three 4-wave
+  blocks per CU, three waves per SIMD: at most 168 (512 / 3 in the allocation
+  granule of 8).
+One register over the bound halves the down GEMM's blocks per CU and the
+2048-row prefill's down kernel goes from about 106 to 125 us with identical
+output bits, which no numerical test sees.
+"""
+import re
+import subprocess
+
+import pytest
+
+from veymoe import build
+
+SOURCE = f"{build.CSRC}/grouped.hip"
+
+
+def _resources(tmp_path):
+    try:
+        hipcc = build.hipcc()
+    except RuntimeError:
+        pytest.skip("hipcc is not installed")
+    cmd = [hipcc, *build.HIP_FLAGS, "--cuda-device-only", "-Rpass-analysis=kernel-resource-usage",
+           "-c", SOURCE, "-o", str(tmp_path / "grouped_device.o")]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    assert proc.returncode == 0, proc.stderr[-2000:]
+    kernels, name = {}, None
+    for line in proc.stderr.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            kernels[name] = {}
+            continue
+        m = re.search(r"remark: +(VGPRs|AGPRs): (\d+)", line)
+        if m and name is not None:
+            kernels[name][m.group(1)] = int(m.group(2))
+    return kernels
+
+
+def _instances(kernels, prefix):
+    found = {k: v for k, v in kernels.items() if prefix in k}
+    assert found, f"no kernel matching {prefix} in the resource report"
+    return found
+
+
+def test_grouped_gemm_register_budgets(tmp_path):
+    kernels = _resources(tmp_path)
+    # down: EPI 1, 8 waves, 2 column blocks per wave, 1 projection, no tail chunk
+    for name, r in _instances(kernels, "k_groupedILi1ELi8ELi2ELi1ELb0E").items():
+        assert r["VGPRs"] + r.get("AGPRs", 0) <= 128, (name, r)
+    # gate/up: EPI 0, 4 waves, 1 column block per wave, 2 projections, no tail chunk
+    for name, r in _instances(kernels, "k_groupedILi0ELi4ELi1ELi2ELb0E").items():
+        assert r["VGPRs"] + r.get("AGPRs", 0) <= 168, (name, r)

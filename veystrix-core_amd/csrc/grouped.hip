@@ -164,17 +164,40 @@ struct Dequant {
     s16 = 0.0625f * s;
     b64 = fmaf(-64.0f, s, b);
   }
+  // EAGER: each pair is packed as soon as it is computed.  The down GEMM
+  // needs it: computing all eight values first held two more VGPRs there
+  // (130), which cost it its second block per CU (2048 rows 125 -> 106 us
+  // with it).  The gate/up GEMM and the 16-row kernels run faster with the
+  // eight values computed first (2048-row gate/up 200.5 -> 195.5 us).
+  template <bool EAGER = false>
   __device__ __forceinline__ void word(uint32_t w, uint32_t magic, uint32_t out[4]) const {
     const uint32_t w8 = w >> 8;
     const uint32_t m[4] = {(w & 0x000F000Fu) | magic, (w & 0x00F000F0u) | magic, (w8 & 0x000F000Fu) | magic,
                            (w8 & 0x00F000F0u) | magic};
+    const f16x2_t h[4] = {__builtin_bit_cast(f16x2_t, m[0]), __builtin_bit_cast(f16x2_t, m[1]),
+                          __builtin_bit_cast(f16x2_t, m[2]), __builtin_bit_cast(f16x2_t, m[3])};
+    // q_n from h[n].x and q_{n+4} from h[n].y, n < 4 (odd n: the high nibble of a byte)
+    auto q = [&](int n, bool high) {
+      const float sc = n & 1 ? s16 : s, bc = n & 1 ? b64 : b1024;
+      return fmaf(sc, static_cast<float>(high ? h[n].y : h[n].x), bc);
+    };
+    if constexpr (EAGER) {
+      if constexpr (kNatural) {
+        out[0] = pack_bf16(q(0, false), q(1, false));
+        out[2] = pack_bf16(q(0, true), q(1, true));
+        out[1] = pack_bf16(q(2, false), q(3, false));
+        out[3] = pack_bf16(q(2, true), q(3, true));
+      } else {
+#pragma unroll
+        for (int n = 0; n < 4; ++n) out[n] = pack_bf16(q(n, false), q(n, true));
+      }
+      return;
+    }
     float lo[4], hi[4];  // q_n and q_{n+4}, n < 4
 #pragma unroll
     for (int n = 0; n < 4; ++n) {
-      const f16x2_t h = __builtin_bit_cast(f16x2_t, m[n]);
-      const float sc = n & 1 ? s16 : s, bc = n & 1 ? b64 : b1024;
-      lo[n] = fmaf(sc, static_cast<float>(h.x), bc);
-      hi[n] = fmaf(sc, static_cast<float>(h.y), bc);
+      lo[n] = q(n, false);
+      hi[n] = q(n, true);
     }
     if constexpr (kNatural) {
       out[0] = pack_bf16(lo[0], lo[1]);
@@ -232,6 +255,7 @@ struct BChunk<true, false> {
     for (int h = 0; h < kHalves; ++h) w[h] = ldg16(wb + wl + h * 64u);
   }
   // s2/b2: the scales/biases of groups kb (low half) and 4 + kb (high half)
+  template <bool EAGER>
   __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t s2, uint32_t b2) const {
     const int h = st >> 2, i = st & 3;
     const float sc = __uint_as_float(h ? s2 & 0xffff0000u : s2 << 16);
@@ -239,7 +263,7 @@ struct BChunk<true, false> {
     const Dequant dq(sc, bi);
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
     uint32_t r[4];
-    dq.word(word, magic, r);
+    dq.template word<EAGER>(word, magic, r);
     return as_operand(r);
   }
 };
@@ -260,12 +284,13 @@ struct BChunk<true, true> {
       b[h] = ldg_u16(reinterpret_cast<const uint8_t*>(p.b) + mrow + g * 2u);
     }
   }
+  template <bool EAGER>
   __device__ __forceinline__ bf16x8_t step(int st, uint32_t magic, uint32_t, uint32_t) const {
     const int h = st >> 2, i = st & 3;
     const Dequant dq(bf16_to_f32(s[h]), bf16_to_f32(b[h]));
     const uint32_t word = i == 0 ? w[h].x : i == 1 ? w[h].y : i == 2 ? w[h].z : w[h].w;
     uint32_t r[4];
-    dq.word(word, magic, r);
+    dq.template word<EAGER>(word, magic, r);
     return as_operand(r);
   }
 };
@@ -284,6 +309,7 @@ struct BChunk<false, TAIL> {
       for (int i = 0; i < 4; ++i) v[h][i] = ldg16(src + 16 * i);
     }
   }
+  template <bool EAGER>
   __device__ __forceinline__ bf16x8_t step(int st, uint32_t, uint32_t, uint32_t) const {
     uint32_t r[4];
     permute_word(v[st >> 2][st & 3], r);
@@ -538,8 +564,10 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
       for (int pj = 0; pj < PROJ; ++pj)
 #pragma unroll
         for (int nb = 0; nb < NBW; ++nb) {
-          const bf16x8_t bop = kLdsB ? bl[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb])
-                                     : bc[pj][nb].step(st, magic, s2[pj][nb], b2[pj][nb]);
+          // the down GEMM packs each dequantised pair as it is computed
+          constexpr bool kEager = EPI == kEpiRows;
+          const bf16x8_t bop = kLdsB ? bl[pj][nb].template step<kEager>(st, magic, s2[pj][nb], b2[pj][nb])
+                                     : bc[pj][nb].template step<kEager>(st, magic, s2[pj][nb], b2[pj][nb]);
 #pragma unroll
           for (int mb = 0; mb < MBU; ++mb)
             acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
@@ -810,6 +838,7 @@ __device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t l
 // at step j the 64 lanes (16 rows x 4 quarters) read units q G/4*4 + j, which
 // this spreads over all 16 bank groups, four lanes each.
 constexpr int kRowsDepth = 3;  // chunks of weight loads in flight per wave
+constexpr int kRowsCG = 8;     // 32-input groups per k_rows chunk (K = 256 KCH)
 
 __device__ __forceinline__ constexpr uint32_t rows_swz(uint32_t r, uint32_t q) { return (r ^ (q << 2)) & 15u; }
 
@@ -841,7 +870,7 @@ template <int EPI, int WAVES, int PROJ, int KCH>
 __device__ __forceinline__ bool rows_item(const GroupedLaunch& p, uint32_t item, uint8_t* s_a, PhaseTrace& tr) {
   constexpr int kThreads = WAVES * 64;
   constexpr int kCols = WAVES * 16;
-  constexpr int kG = KCH * 8;                      // groups of K
+  constexpr int kG = KCH * kRowsCG;                // groups of K
   constexpr int kQG = kG / 4;                      // groups per lane quarter (2 KCH)
   constexpr int kUnits = kG * 4;                   // 16-byte A units per row
   constexpr int kRowBytes = kUnits * 16;
@@ -1489,7 +1518,7 @@ bool rows_supported(uint32_t k_dim) {
 template <int EPI, int WAVES, int PROJ, int KCH>
 hipError_t rows_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
   auto kernel = &k_rows<EPI, WAVES, PROJ, KCH>;
-  constexpr uint32_t lds = 16u * KCH * kCG * kGroup * 2u;
+  constexpr uint32_t lds = 16u * KCH * kRowsCG * kGroup * 2u;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
