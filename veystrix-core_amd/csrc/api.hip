@@ -546,12 +546,20 @@ static bool small_grouped(uint32_t T, uint32_t H, uint32_t I) {
   return VM_ROWS_PATH && T <= kRowsMaxTokens && vm::rows_supported(H) && vm::rows_supported(I);
 }
 
+// Rows per gate/up tile of a chunked-GEMM call: tall tiles when the routed
+// experts average more than kTallRowsPerGroup rows and the hidden size is a
+// whole number of K chunks (the tall instance has no tail chunk).
+static uint32_t gateup_tile_rows(uint32_t T, uint32_t K, uint32_t H, uint32_t E) {
+  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kTallRowsPerGroup && H % (8 * 32) == 0;
+  return tall ? vm::kGroupedRowsTall : vm::kGroupedRows;
+}
+
 static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint32_t E, bool shared) {
   GroupedWs w{};
   w.rows_total = T * K + (shared ? T : 0);
   w.groups = E + (shared ? 1 : 0);
   w.small = small_grouped(T, H, I);
-  w.tile_rows = w.small ? vm::kRowsTile : vm::kGroupedRows;
+  w.tile_rows = w.small ? vm::kRowsTile : gateup_tile_rows(T, K, H, E);
   w.tile_rows_dn = w.small ? vm::kRowsTile : vm::kGroupedRowsDown;
   w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows);
   w.max_tiles_dn = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows_dn);
@@ -1116,7 +1124,8 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.a_stride = g.H;
   q.a_rows = g.T;
   // routed rows per expert on average: at most one row tile each
-  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * vm::kGroupedRows;
+  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * w.tile_rows;
+  q.tile_rows = w.small ? 0u : w.tile_rows;
   e = w.small ? vm::launch_rows(vm::kEpiSwiglu, q, w.max_tiles, stream)
               : vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
   if (e != hipSuccess) return hip_fail(e, "grouped gate/up launch");
@@ -1134,6 +1143,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.a_stride = g.I;
   q.a_rows = g.T * g.K + (g.shared ? g.T : 0);
   q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * vm::kGroupedRowsDown;
+  q.tile_rows = 0;  // the down GEMM's own tile height
   q.tiles = s.tiles_dn;
   q.tile_count = s.tile_count_dn;
   e = w.small ? vm::launch_rows(vm::kEpiRows, q, w.max_tiles_dn, stream)
@@ -1189,9 +1199,13 @@ static hipError_t launch_shared_expert(const VmLayerArgs* a, uint16_t* sig, uint
   q.n_dim = I;
   q.a_stride = H;
   q.a_rows = T;
-  e = vm::launch_grouped(vm::kEpiSwiglu, q, (T + vm::kGroupedRows - 1) / vm::kGroupedRows, stream);
+  // the same tile height as the call's routed gate/up
+  const uint32_t tr = gateup_tile_rows(T, a->top_k, H, a->expert_count);
+  q.tile_rows = tr == vm::kGroupedRows ? 0u : tr;
+  e = vm::launch_grouped(vm::kEpiSwiglu, q, (T + tr - 1) / tr, stream);
   if (e != hipSuccess) return e;
   q.a = sh_act;
+  q.tile_rows = 0;
   q.shared[0] = to_ptrs(a->shared_down_proj);
   q.shared[1] = vm::ProjPtrs{};
   q.part[0] = 2;

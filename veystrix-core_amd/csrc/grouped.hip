@@ -110,9 +110,9 @@ constexpr int tile_rows() {
   return EPI == kEpiRows ? kGroupedRowsDown : EPI == kEpiLogits ? kGroupedRowsRouter : kGroupedRows;
 }
 
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int TR = tile_rows<EPI>()>
 constexpr int stage_bytes() {
-  return tile_rows<EPI>() * row_bytes<EPI>() + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
+  return TR * row_bytes<EPI>() + (EPI != kEpiLogits && !TAIL ? PROJ * 2 * WAVES * NBW * 16 * 16 : 0) +
          (lds_weights<EPI, TAIL>() ? PROJ * WAVES * NBW * 16 * kWColBytes : 0);
 }
 
@@ -339,7 +339,7 @@ constexpr uint32_t slices_per_block() {
 // staging covers those rows only and the MFMA loops carry no branch, so the
 // LDS reads of a step and the MFMAs of neighbouring steps can be scheduled
 // freely.
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU, bool WNT>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, int MBU, bool WNT, int TR>
 __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjPtrs (&w)[PROJ], uint32_t row0,
                                              uint32_t rows, uint32_t slice0, uint32_t nslices, uint8_t* s_a0) {
   constexpr bool Q4 = EPI != kEpiLogits;
@@ -394,8 +394,8 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   constexpr bool kLdsScales = Q4 && !TAIL;
   constexpr int kSVecs = kLdsScales ? PROJ * 2 * kCols : 0;
   constexpr int kSItems = (kSVecs + kThreads - 1) / kThreads;
-  constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
-  constexpr int kStageBytes = tile_rows<EPI>() * kRowB;  // the A rows of a stage
+  constexpr int kStage = stage_bytes<EPI, WAVES, NBW, PROJ, TAIL, TR>();
+  constexpr int kStageBytes = TR * kRowB;  // the A rows of a stage
   const uint8_t* sv_base[kSItems > 0 ? kSItems : 1];  // wave-uniform
   uint32_t sv_vo[kSItems > 0 ? kSItems : 1];
 #pragma unroll
@@ -692,7 +692,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   }
 }
 
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT, int TR>
 __device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t lin, uint8_t* s_a0);
 
 // EPI: 0 SwiGLU of projections 0 (gate) and 1 (up) -> bf16 [rows, N];
@@ -719,11 +719,11 @@ __device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t l
 // 2048-row gate/up fetched 28 % above its bytes).  Calls with several row
 // tiles per expert keep cached loads (the tiles of an expert share its
 // weights in the L2; non-temporal loads there cost 5 %).
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT, int TR>
 __global__ __launch_bounds__(WAVES * 64)
 __attribute__((amdgpu_waves_per_eu(EPI == kEpiRows ? VM_DN_WAVES_PER_EU : VM_G_WAVES_PER_EU)))
 void k_grouped(GroupedLaunch p) {
-  static_assert(tile_rows<EPI>() % 16 == 0 && tile_rows<EPI>() <= 64, "tiles are one to four 16-row blocks");
+  static_assert(TR % 16 == 0 && TR <= 96, "tiles are one to six 16-row blocks");
   extern __shared__ uint4 s_dyn[];  // two stages of stage_bytes<...>()
   uint8_t* s_a0 = reinterpret_cast<uint8_t*>(s_dyn);
   const uint32_t tid = threadIdx.x;
@@ -740,13 +740,13 @@ void k_grouped(GroupedLaunch p) {
     if (blockIdx.x == 0 && p.zero_words != nullptr)
       for (uint32_t i = tid; i < p.zero_count; i += WAVES * 64) p.zero_words[i] = 0;
   }
-  grouped_block<EPI, WAVES, NBW, PROJ, TAIL, WNT>(p, blockIdx.x, s_a0);
+  grouped_block<EPI, WAVES, NBW, PROJ, TAIL, WNT, TR>(p, blockIdx.x, s_a0);
 }
 
 // One block's work item `lin` (the XCD-aware order of k_grouped).
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT, int TR>
 __device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t lin, uint8_t* s_a0) {
-  constexpr int kBM = tile_rows<EPI>();
+  constexpr int kBM = TR;
   constexpr int kMB = kBM / 16;  // MFMA row blocks
   constexpr bool Q4 = EPI != kEpiLogits;
   const uint32_t tid = threadIdx.x;
@@ -806,16 +806,22 @@ __device__ __forceinline__ void grouped_block(const GroupedLaunch& p, uint32_t l
     }
   }
   const uint32_t mbu = (rows + 15) / 16;  // block-uniform, 1..kMB
+  if constexpr (kMB >= 6) {
+    if (mbu >= 6) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 6, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
+  }
+  if constexpr (kMB >= 5) {
+    if (mbu >= 5) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 5, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
+  }
   if constexpr (kMB >= 4) {
-    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu >= 4) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 4, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 3) {
-    if (mbu == 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu >= 3) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 3, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
   }
   if constexpr (kMB >= 2) {
-    if (mbu == 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
+    if (mbu >= 2) return grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 2, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
   }
-  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1, WNT>(p, w, row0, rows, slice0, nslices, s_a0);
+  grouped_tile<EPI, WAVES, NBW, PROJ, TAIL, 1, WNT, TR>(p, w, row0, rows, slice0, nslices, s_a0);
 }
 
 // ------------------------------------------------------------- row tiles ---
@@ -1429,11 +1435,12 @@ hipError_t launch(const char* family, void (*kernel)(KArgs...), dim3 grid, dim3 
   return hipGetLastError();
 }
 
-template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT>
+template <int EPI, int WAVES, int NBW, int PROJ, bool TAIL, bool WNT, int TR = tile_rows<EPI>()>
 hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
   // one LDS stage with staged weights (see grouped_tile), else two
-  constexpr uint32_t lds = (lds_weights<EPI, TAIL>() ? 1 : 2) * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL>();
-  auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL, WNT>;
+  constexpr uint32_t lds = (lds_weights<EPI, TAIL>() ? 1 : 2) * stage_bytes<EPI, WAVES, NBW, PROJ, TAIL, TR>();
+  static_assert(lds <= 160u * 1024u, "the LDS of one block");
+  auto kernel = &k_grouped<EPI, WAVES, NBW, PROJ, TAIL, WNT, TR>;
   static bool attr = false;  // one attribute call per kernel instance
   if (!attr) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
@@ -1459,6 +1466,16 @@ hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max
 
 template <int EPI, int WAVES, int NBW, int PROJ>
 hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
+  if constexpr (EPI == kEpiSwiglu) {
+    // tall tiles: calls of many rows per group, whose groups then need fewer
+    // row tiles (each tile dequantises its expert's weights once); full
+    // chunks and cached weight loads only
+    if (p.tile_rows == static_cast<uint32_t>(kGroupedRowsTall)) {
+      if ((p.k_dim / kGroup) % kCG != 0 || p.weights_once) return hipErrorInvalidValue;
+      return grouped_go_k<EPI, WAVES, NBW, PROJ, false, false, kGroupedRowsTall>(family, p, max_tiles, stream);
+    }
+  }
+  if (p.tile_rows != 0 && p.tile_rows != static_cast<uint32_t>(tile_rows<EPI>())) return hipErrorInvalidValue;
   if ((p.k_dim / kGroup) % kCG != 0)
     return grouped_go_k<EPI, WAVES, NBW, PROJ, true, false>(family, p, max_tiles, stream);
   if (lds_weights<EPI, false>() && p.weights_once)

@@ -209,6 +209,15 @@ hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 #define VM_GROUPED_ROWS_RT 64
 #endif
 constexpr int kGroupedRows = VM_GROUPED_ROWS;
+// gate/up tiles of calls with more than kTallRowsPerGroup rows per routed
+// expert on average (the 8192-row window: ~160), so that a group takes two
+// tiles instead of three and its weights are dequantised twice, not three
+// times (the block then runs two per CU instead of three)
+#ifndef VM_GROUPED_ROWS_TALL
+#define VM_GROUPED_ROWS_TALL 96
+#endif
+constexpr int kGroupedRowsTall = VM_GROUPED_ROWS_TALL;
+constexpr uint32_t kTallRowsPerGroup = 128;
 constexpr int kGroupedRowsDown = VM_GROUPED_ROWS_DN;
 constexpr int kGroupedRowsRouter = VM_GROUPED_ROWS_RT;  // router GEMM tiles (no sort: rows in order)
 constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
@@ -237,6 +246,7 @@ struct GroupedLaunch {
   uint32_t k_dim, n_dim, experts, a_stride;
   uint32_t a_rows;             // rows of the A matrix: the chunked GEMM addresses it with 32-bit byte offsets
   uint32_t spb;                // column slices per block (set by launch_grouped)
+  uint32_t tile_rows;          // rows per tile of `tiles`: 0 the instance's own, or kGroupedRowsTall (gate/up)
   bool weights_once;           // most groups hold one row tile: stream the weights past the L2
   // router GEMM only: block 0 zeroes zero_count words at zero_words (the
   // counters of the sort that follows the select)
