@@ -90,19 +90,28 @@ def test_grouped_layer_small(device, tokens):
     _assert_layer(host(y), spec, seed, x_np, rows, same, ref, f"grouped layer T={tokens}")
 
 
-def test_grouped_layer_many_rows_per_expert(device):
-    """2048 tokens over 64 experts: ~128 rows per expert, several row tiles per group."""
+@pytest.mark.parametrize("tokens", [2048, 4096])
+def test_grouped_layer_many_rows_per_expert(device, tokens):
+    """2048 or 4096 tokens over 64 experts top-4: ~128 or ~256 rows per
+    expert, several row tiles per group.  Above 128 rows per expert on
+    average the gate/up GEMM takes 96-row tiles (4096 tokens here) instead of
+    64-row ones; a row's result does not depend on its tile, so the first 2048
+    rows of the 4096-row call equal the 2048-row call bit for bit."""
     spec = synth.CONFIGS["decode_small"]
     seed = 311
     layer = assemble.build_layer(spec, seed, device, dense=True)
-    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, 2048))
+    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
     y = layer(bf16_device(x_np, device))
     torch.cuda.synchronize()
-    sample = np.random.default_rng(1).choice(2048, 48, replace=False)
+    sample = np.random.default_rng(1).choice(tokens, 48, replace=False)
     ref = _layer_ref(spec, seed, x_np, sample)
     inds = layer.last_inds.cpu().numpy()[sample]
-    same = _check_selection(inds, ref, spec.top_k, 3, "T=2048 over 64 experts")
-    _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, "grouped layer T=2048 (sample)")
+    same = _check_selection(inds, ref, spec.top_k, 3, f"T={tokens} over 64 experts")
+    _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, f"grouped layer T={tokens} (sample)")
+    if tokens > 2048:
+        first = layer(bf16_device(x_np[:2048], device))
+        torch.cuda.synchronize()
+        assert torch.equal(first.view(torch.int16), y[:2048].view(torch.int16))
 
 
 @pytest.mark.parametrize("hidden,experts,tokens,zipf", [(4096, 128, 300, None), (4096, 128, 8256, None),
