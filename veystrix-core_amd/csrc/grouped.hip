@@ -1301,20 +1301,74 @@ __global__ __launch_bounds__(1024) void k_sort_place(SortLaunch p) {
 
 // --------------------------------------------------------------- combine ---
 
+// A token's value of a [tokens, ...] array.  UNIFORM: the address is the same
+// in every lane of the wave, and the value is read through the scalar data
+// cache into SGPRs (the arrays read this way are written by earlier
+// launches only).
+template <bool UNIFORM>
+__device__ __forceinline__ uint32_t token_u32(const uint32_t* p, size_t i) {
+  if constexpr (UNIFORM) return *(const __attribute__((address_space(4))) uint32_t*)(p + i);
+  else return p[i];
+}
+// Element i of a bf16 (dtype 0) or fp32 array in two steps, so that a scalar
+// load's wait comes at the value's first use rather than at the load: the
+// raw dword (UNIFORM: the aligned dword holding a bf16 element, which never
+// crosses a page) and its conversion.
+struct TokenRaw {
+  uint32_t w, high;
+};
+template <bool UNIFORM>
+__device__ __forceinline__ TokenRaw token_raw(const void* p, size_t i, uint32_t dtype) {
+  if constexpr (UNIFORM) {
+    if (dtype != 0) return {token_u32<true>(static_cast<const uint32_t*>(p), i), 2u};
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p) + 2u * i;
+    return {*(const __attribute__((address_space(4))) uint32_t*)(a & ~static_cast<uintptr_t>(3)),
+            static_cast<uint32_t>(a & 2u) >> 1};
+  } else {
+    return {dtype != 0 ? ldg_u32(static_cast<const float*>(p) + i) : ldg_u16(static_cast<const uint16_t*>(p) + i),
+            dtype != 0 ? 2u : 0u};
+  }
+}
+// high: 0 low bf16 half, 1 high bf16 half, 2 fp32
+__device__ __forceinline__ float token_value(TokenRaw r) {
+  return r.high == 2u ? __uint_as_float(r.w) : bf16_to_f32(r.high ? r.w >> 16 : r.w & 0xffffu);
+}
+template <bool UNIFORM>
+__device__ __forceinline__ float token_any(const void* p, size_t i, uint32_t dtype) {
+  return token_value(token_raw<UNIFORM>(p, i, dtype));
+}
+
 // One thread per 8 outputs of one token.  mode 1 (generic): products rounded,
 // summed in slot order in fp32, rounded; mode 0 (fused): fp32 sum of
 // round(down) * score.  Then + round(sigmoid gate * shared) or + shared_y.
 // mode 2: no combine, out[t, j] = the slot's expert output row.
+// WAVE_TOKEN (hidden / 8 a multiple of 64): the 64 threads of a wave hold
+// outputs of one token, so its row indices, scores and gates are scalar
+// loads and each row load is an SGPR base plus the lane's offset; the
+// registers that frees let every wave of a 2048-token call be resident at
+// once (at most 64 VGPRs: eight waves per SIMD).
+template <bool WAVE_TOKEN>
 __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
   const uint32_t per_token = p.hidden / 8;
   const uint32_t i = blockIdx.x * kGB + threadIdx.x;
   if (i >= p.tokens * per_token) return;
-  const uint32_t t = i / per_token, h0 = (i % per_token) * 8;
+  uint32_t t = i / per_token;
+  if constexpr (WAVE_TOKEN) t = __builtin_amdgcn_readfirstlane(t);
+  const uint32_t h0 = (i % per_token) * 8;
+  // the pointers the first loads need, read from the arguments together, so
+  // that the token's index loads and the shared row's are issued together
+  const uint32_t* pair_row = p.pair_row;
+  const uint32_t* shared_first = p.shared_first;
+  VM_KEEP(pair_row);
+  VM_KEEP(shared_first);
+  const uint32_t voff = h0 * 2u;  // the lane's byte offset in a row
+  auto row_ptr = [&](uint32_t row) {
+    return reinterpret_cast<const uint8_t*>(p.rows + static_cast<size_t>(row) * p.hidden) + voff;
+  };
   if (p.mode == 2) {  // no combine: every slot's rounded expert output
     for (uint32_t j = 0; j < p.slots; ++j) {
-      const uint32_t row = p.pair_row[t * p.slots + j];
-      const uint4 v = row == kNoRow ? make_uint4(0, 0, 0, 0)
-                                    : ldg16(p.rows + static_cast<size_t>(row) * p.hidden + h0);
+      const uint32_t row = token_u32<WAVE_TOKEN>(pair_row, static_cast<size_t>(t) * p.slots + j);
+      const uint4 v = row == kNoRow ? make_uint4(0, 0, 0, 0) : ldg16(row_ptr(row));
       *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.out) + (static_cast<size_t>(t) * p.slots + j) * p.hidden +
                                 h0) = v;
     }
@@ -1325,29 +1379,34 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
   // thread waits for one round trip of each kind rather than one per slot
   uint32_t row[kCombineSlots];
   float sc[kCombineSlots];
+  const uint32_t first = shared_first != nullptr ? token_u32<WAVE_TOKEN>(shared_first, 0) : 0u;
 #pragma unroll
   for (int j = 0; j < kCombineSlots; ++j)
-    row[j] = j < static_cast<int>(p.slots) ? p.pair_row[t * p.slots + j] : kNoRow;
+    row[j] = j < static_cast<int>(p.slots) ? token_u32<WAVE_TOKEN>(pair_row, static_cast<size_t>(t) * p.slots + j)
+                                           : kNoRow;
   uint4 sh = make_uint4(0, 0, 0, 0);
-  float sig = 0.0f;
-  const uint16_t* shr =
-      p.shared_first != nullptr ? p.rows + static_cast<size_t>(*p.shared_first) * p.hidden : p.shared_rows;
+  TokenRaw sig_raw{0u, 2u};
+  const uint16_t* shr = shared_first != nullptr ? p.rows + static_cast<size_t>(first) * p.hidden : p.shared_rows;
   if (shr != nullptr) {
-    sh = ldg16(shr + static_cast<size_t>(t) * p.hidden + h0);
-    sig = ActBF16::load(p.shared_sig, t);
+    sh = ldg16(reinterpret_cast<const uint8_t*>(shr + static_cast<size_t>(t) * p.hidden) + voff);
+    sig_raw = token_raw<WAVE_TOKEN>(p.shared_sig, t, 0);
   } else if (p.shared_y != nullptr) {
-    sh = ldg16(static_cast<const uint16_t*>(p.shared_y) + static_cast<size_t>(t) * p.hidden + h0);
+    sh = ldg16(reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.shared_y) +
+                                                static_cast<size_t>(t) * p.hidden) + voff);
   }
   uint4 v[kCombineSlots];
 #pragma unroll
-  for (int j = 0; j < kCombineSlots; ++j) {
-    sc[j] = row[j] != kNoRow ? load_any(p.scores, static_cast<size_t>(t) * p.slots + j, p.score_dtype) : 0.0f;
-    v[j] = row[j] != kNoRow ? ldg16(p.rows + static_cast<size_t>(row[j]) * p.hidden + h0) : make_uint4(0, 0, 0, 0);
-  }
+  for (int j = 0; j < kCombineSlots; ++j) v[j] = row[j] != kNoRow ? ldg16(row_ptr(row[j])) : make_uint4(0, 0, 0, 0);
+  TokenRaw sr[kCombineSlots];
+#pragma unroll
+  for (int j = 0; j < kCombineSlots; ++j)
+    sr[j] = row[j] != kNoRow ? token_raw<WAVE_TOKEN>(p.scores, static_cast<size_t>(t) * p.slots + j, p.score_dtype)
+                             : TokenRaw{0u, 2u};
   float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
   for (int j = 0; j < kCombineSlots; ++j) {
     if (row[j] == kNoRow) continue;
+    sc[j] = token_value(sr[j]);
     const uint32_t words[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -1356,6 +1415,7 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
       acc[e] = __fadd_rn(acc[e], p.mode == 1 ? round_bf16(prod) : prod);
     }
   }
+  const float sig = token_value(sig_raw);
   uint32_t out[4];
   const uint32_t shw[4] = {sh.x, sh.y, sh.z, sh.w};
 #pragma unroll
@@ -1381,7 +1441,7 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
   for (int e = 0; e < 8; ++e) y[e] = bf16_to_f32(e & 1 ? out[e / 2] >> 16 : out[e / 2] & 0xffffu);
   for (uint32_t j = 0; j < inj.hc; ++j) {
     const size_t o = (static_cast<size_t>(t) * inj.hc + j) * p.hidden + h0;
-    const float w = ActBF16::load(inj.weights, static_cast<size_t>(t) * inj.hc + j);
+    const float w = token_any<WAVE_TOKEN>(inj.weights, static_cast<size_t>(t) * inj.hc + j, 0);
     const uint4 hv = ldg16(static_cast<const uint16_t*>(inj.hidden) + o);
     const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w};
     uint32_t res[4];
@@ -1605,7 +1665,9 @@ hipError_t launch_sort_counted(const SortLaunch& p, hipStream_t stream) {
 hipError_t launch_grouped_combine(const CombineLaunch& p, hipStream_t stream) {
   if (p.slots == 0 || p.slots > static_cast<uint32_t>(kCombineSlots)) return hipErrorInvalidValue;
   const uint32_t n = p.tokens * (p.hidden / 8);
-  return launch("combine", k_grouped_combine, dim3((n + kGB - 1) / kGB), dim3(kGB), stream, p);
+  if ((p.hidden / 8) % 64 == 0)
+    return launch("combine", k_grouped_combine<true>, dim3((n + kGB - 1) / kGB), dim3(kGB), stream, p);
+  return launch("combine", k_grouped_combine<false>, dim3((n + kGB - 1) / kGB), dim3(kGB), stream, p);
 }
 
 hipError_t launch_shared_gate(const uint16_t* x, const ProjPtrs& seg, uint16_t* sig, uint32_t tokens,
