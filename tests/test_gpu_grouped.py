@@ -90,6 +90,25 @@ def test_grouped_layer_small(device, tokens):
     _assert_layer(host(y), spec, seed, x_np, rows, same, ref, f"grouped layer T={tokens}")
 
 
+@pytest.mark.parametrize("tokens", [130, 300])
+def test_grouped_layer_narrow_hidden_with_shared_expert(device, tokens):
+    """Hidden 256 with a shared expert above 64 rows: the shared expert runs
+    on the side stream and the combine reads its rows and sigmoid gates back.
+    At this width a token's 32 combine threads share a wave with another
+    token's, so the combine takes its per-lane loads (wider layers read a
+    token's indices, scores and gate through scalar loads)."""
+    spec = synth.LayerSpec("narrow_shared", 256, 128, 64, 4, 128, 1)
+    seed = 320 + tokens
+    layer = assemble.build_layer(spec, seed, device, dense=True)
+    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
+    y = layer(bf16_device(x_np, device))
+    torch.cuda.synchronize()
+    rows = np.arange(tokens)
+    ref = _layer_ref(spec, seed, x_np, rows)
+    same = _check_selection(layer.last_inds.cpu().numpy(), ref, spec.top_k, max(1, tokens // 20), f"T={tokens}")
+    _assert_layer(host(y), spec, seed, x_np, rows, same, ref, f"narrow grouped layer T={tokens}")
+
+
 @pytest.mark.parametrize("tokens", [2048, 4096])
 def test_grouped_layer_many_rows_per_expert(device, tokens):
     """2048 or 4096 tokens over 64 experts top-4: ~128 or ~256 rows per
