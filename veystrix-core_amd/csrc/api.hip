@@ -554,13 +554,19 @@ static uint32_t gateup_tile_rows(uint32_t T, uint32_t K, uint32_t H, uint32_t E)
   return tall ? vm::kGroupedRowsTall : vm::kGroupedRows;
 }
 
+// Rows per down tile: the same rule over the intermediate size.
+static uint32_t down_tile_rows(uint32_t T, uint32_t K, uint32_t I, uint32_t E) {
+  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kTallRowsPerGroup && I % (8 * 32) == 0;
+  return tall ? vm::kGroupedRowsTall : vm::kGroupedRowsDown;
+}
+
 static GroupedWs grouped_ws(uint32_t T, uint32_t K, uint32_t H, uint32_t I, uint32_t E, bool shared) {
   GroupedWs w{};
   w.rows_total = T * K + (shared ? T : 0);
   w.groups = E + (shared ? 1 : 0);
   w.small = small_grouped(T, H, I);
   w.tile_rows = w.small ? vm::kRowsTile : gateup_tile_rows(T, K, H, E);
-  w.tile_rows_dn = w.small ? vm::kRowsTile : vm::kGroupedRowsDown;
+  w.tile_rows_dn = w.small ? vm::kRowsTile : down_tile_rows(T, K, I, E);
   w.max_tiles = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows);
   w.max_tiles_dn = vm::grouped_max_tiles(w.rows_total, w.groups, w.tile_rows_dn);
   uint64_t o = kAlign;
@@ -1143,7 +1149,7 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.a_stride = g.I;
   q.a_rows = g.T * g.K + (g.shared ? g.T : 0);
   q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * vm::kGroupedRowsDown;
-  q.tile_rows = 0;  // the down GEMM's own tile height
+  q.tile_rows = w.small || w.tile_rows_dn == vm::kGroupedRowsDown ? 0u : w.tile_rows_dn;
   q.tiles = s.tiles_dn;
   q.tile_count = s.tile_count_dn;
   e = w.small ? vm::launch_rows(vm::kEpiRows, q, w.max_tiles_dn, stream)
@@ -1199,13 +1205,18 @@ static hipError_t launch_shared_expert(const VmLayerArgs* a, uint16_t* sig, uint
   q.n_dim = I;
   q.a_stride = H;
   q.a_rows = T;
-  // the same tile height as the call's routed gate/up
+  // the same tile height as the call's routed gate/up (tall tiles by the
+  // shared expert's own T rows measured no faster)
   const uint32_t tr = gateup_tile_rows(T, a->top_k, H, a->expert_count);
   q.tile_rows = tr == vm::kGroupedRows ? 0u : tr;
   e = vm::launch_grouped(vm::kEpiSwiglu, q, (T + tr - 1) / tr, stream);
   if (e != hipSuccess) return e;
   q.a = sh_act;
-  q.tile_rows = 0;
+  // its own group of T rows: tall tiles above kTallRowsPerGroup rows (each
+  // weight dequantised half as often, which leaves the routed gate/up it runs
+  // beside more of the CUs)
+  const uint32_t trd = down_tile_rows(T, 1, I, 1);
+  q.tile_rows = trd == vm::kGroupedRowsDown ? 0u : trd;
   q.shared[0] = to_ptrs(a->shared_down_proj);
   q.shared[1] = vm::ProjPtrs{};
   q.part[0] = 2;
@@ -1213,7 +1224,7 @@ static hipError_t launch_shared_expert(const VmLayerArgs* a, uint16_t* sig, uint
   q.k_dim = I;
   q.n_dim = H;
   q.a_stride = I;
-  return vm::launch_grouped(vm::kEpiRows, q, (T + vm::kGroupedRowsDown - 1) / vm::kGroupedRowsDown, stream);
+  return vm::launch_grouped(vm::kEpiRows, q, (T + trd - 1) / trd, stream);
 }
 
 static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {

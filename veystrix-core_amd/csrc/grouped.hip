@@ -1526,7 +1526,7 @@ hipError_t grouped_go_k(const char* family, const GroupedLaunch& p, uint32_t max
 
 template <int EPI, int WAVES, int NBW, int PROJ>
 hipError_t grouped_go(const char* family, const GroupedLaunch& p, uint32_t max_tiles, hipStream_t stream) {
-  if constexpr (EPI == kEpiSwiglu) {
+  if constexpr (EPI == kEpiSwiglu || EPI == kEpiRows) {
     // tall tiles: calls of many rows per group, whose groups then need fewer
     // row tiles (each tile dequantises its expert's weights once); full
     // chunks and cached weight loads only

@@ -209,10 +209,12 @@ hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 #define VM_GROUPED_ROWS_RT 64
 #endif
 constexpr int kGroupedRows = VM_GROUPED_ROWS;
-// gate/up tiles of calls with more than kTallRowsPerGroup rows per routed
-// expert on average (the 8192-row window: ~160), so that a group takes two
-// tiles instead of three and its weights are dequantised twice, not three
-// times (the block then runs two per CU instead of three)
+// gate/up and down tiles of calls with more than kTallRowsPerGroup rows per
+// routed expert on average (the 8192-row window: ~160), so that a group takes
+// two tiles instead of three (gate/up) or four (down) and its weights are
+// dequantised that much less often; the blocks then run two per CU instead of
+// three (gate/up) and one instead of two (down).  The shared expert's down
+// takes them above kTallRowsPerGroup rows of its own.
 #ifndef VM_GROUPED_ROWS_TALL
 #define VM_GROUPED_ROWS_TALL 96
 #endif
