@@ -109,28 +109,32 @@ def test_grouped_layer_narrow_hidden_with_shared_expert(device, tokens):
     _assert_layer(host(y), spec, seed, x_np, rows, same, ref, f"narrow grouped layer T={tokens}")
 
 
-@pytest.mark.parametrize("tokens", [2048, 4096])
-def test_grouped_layer_many_rows_per_expert(device, tokens):
-    """2048 or 4096 tokens over 64 experts top-4: ~128 or ~256 rows per
-    expert, several row tiles per group.  Above 128 rows per expert on
-    average the gate/up GEMM takes 96-row tiles (4096 tokens here) instead of
-    64-row ones; a row's result does not depend on its tile, so the first 2048
-    rows of the 4096-row call equal the 2048-row call bit for bit."""
+def test_grouped_layer_tile_heights_agree(device):
+    """768, 1024 and 4096 tokens over 64 experts top-4: 48, 64 and 256 rows
+    per expert on average.  A call whose experts average more rows than one
+    tile of the usual height holds takes 96-row tiles: neither GEMM at 768
+    tokens, the down GEMM at 1024 (above its 48), both at 4096 (several row
+    tiles per group).  Each call is checked against the oracle on a sample,
+    and a row's result does not depend on its tile, so the first 768 rows of
+    every call are equal bit for bit."""
     spec = synth.CONFIGS["decode_small"]
     seed = 311
     layer = assemble.build_layer(spec, seed, device, dense=True)
-    x_np = mo.bf16_bits_to_f32(synth.tokens(spec, seed, tokens))
-    y = layer(bf16_device(x_np, device))
-    torch.cuda.synchronize()
-    sample = np.random.default_rng(1).choice(tokens, 48, replace=False)
-    ref = _layer_ref(spec, seed, x_np, sample)
-    inds = layer.last_inds.cpu().numpy()[sample]
-    same = _check_selection(inds, ref, spec.top_k, 3, f"T={tokens} over 64 experts")
-    _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, f"grouped layer T={tokens} (sample)")
-    if tokens > 2048:
-        first = layer(bf16_device(x_np[:2048], device))
+    x_all = mo.bf16_bits_to_f32(synth.tokens(spec, seed, 4096))
+    first = None
+    for tokens in (768, 1024, 4096):
+        x_np = x_all[:tokens]
+        y = layer(bf16_device(x_np, device))
         torch.cuda.synchronize()
-        assert torch.equal(first.view(torch.int16), y[:2048].view(torch.int16))
+        sample = np.random.default_rng(tokens).choice(tokens, 48, replace=False)
+        ref = _layer_ref(spec, seed, x_np, sample)
+        inds = layer.last_inds.cpu().numpy()[sample]
+        same = _check_selection(inds, ref, spec.top_k, 3, f"T={tokens} over 64 experts")
+        _assert_layer(host(y)[sample], spec, seed, x_np, sample, same, ref, f"grouped layer T={tokens} (sample)")
+        if first is None:
+            first = y[:768].clone()
+        else:
+            assert torch.equal(first.view(torch.int16), y[:768].view(torch.int16)), tokens
 
 
 @pytest.mark.parametrize("hidden,experts,tokens,zipf", [(4096, 128, 300, None), (4096, 128, 8256, None),

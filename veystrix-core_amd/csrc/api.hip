@@ -547,16 +547,19 @@ static bool small_grouped(uint32_t T, uint32_t H, uint32_t I) {
 }
 
 // Rows per gate/up tile of a chunked-GEMM call: tall tiles when the routed
-// experts average more than kTallRowsPerGroup rows and the hidden size is a
-// whole number of K chunks (the tall instance has no tail chunk).
+// experts average more rows than one tile of the usual height holds and the
+// hidden size is a whole number of K chunks (the tall instance has no tail
+// chunk).  Measured at 512 experts top-10: 3584 rows 592-594 -> 546 us per
+// call, 4096 rows 642-650 -> 581-589 us, no change at 2048 or 8192 rows.
 static uint32_t gateup_tile_rows(uint32_t T, uint32_t K, uint32_t H, uint32_t E) {
-  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kTallRowsPerGroup && H % (8 * 32) == 0;
+  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kGroupedRows && H % (8 * 32) == 0;
   return tall ? vm::kGroupedRowsTall : vm::kGroupedRows;
 }
 
-// Rows per down tile: the same rule over the intermediate size.
+// Rows per down tile: the same rule over the intermediate size and the down
+// GEMM's usual height (3072 rows 514-519 -> 502-508 us per call).
 static uint32_t down_tile_rows(uint32_t T, uint32_t K, uint32_t I, uint32_t E) {
-  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kTallRowsPerGroup && I % (8 * 32) == 0;
+  const bool tall = uint64_t(T) * K > uint64_t(E) * vm::kGroupedRowsDown && I % (8 * 32) == 0;
   return tall ? vm::kGroupedRowsTall : vm::kGroupedRowsDown;
 }
 
@@ -1130,7 +1133,9 @@ static int run_grouped_experts(const GroupedExperts& g, const GroupedWs& w, char
   q.a_stride = g.H;
   q.a_rows = g.T;
   // routed rows per expert on average: at most one row tile each
-  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * w.tile_rows;
+  // (the tall instance loads its weights through the caches: an expert's
+  // tiles, and its gate and up halves' column slices, share them)
+  q.weights_once = uint64_t(g.T) * g.K <= uint64_t(g.E) * w.tile_rows && w.tile_rows != vm::kGroupedRowsTall;
   q.tile_rows = w.small ? 0u : w.tile_rows;
   e = w.small ? vm::launch_rows(vm::kEpiSwiglu, q, w.max_tiles, stream)
               : vm::launch_grouped(vm::kEpiSwiglu, q, w.max_tiles, stream);
@@ -1212,7 +1217,7 @@ static hipError_t launch_shared_expert(const VmLayerArgs* a, uint16_t* sig, uint
   e = vm::launch_grouped(vm::kEpiSwiglu, q, (T + tr - 1) / tr, stream);
   if (e != hipSuccess) return e;
   q.a = sh_act;
-  // its own group of T rows: tall tiles above kTallRowsPerGroup rows (each
+  // its own group of T rows: tall tiles above 48 rows (each
   // weight dequantised half as often, which leaves the routed gate/up it runs
   // beside more of the CUs)
   const uint32_t trd = down_tile_rows(T, 1, I, 1);

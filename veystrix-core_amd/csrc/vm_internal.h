@@ -209,17 +209,16 @@ hipError_t launch_fill(const FillLaunch& p, hipStream_t stream);
 #define VM_GROUPED_ROWS_RT 64
 #endif
 constexpr int kGroupedRows = VM_GROUPED_ROWS;
-// gate/up and down tiles of calls with more than kTallRowsPerGroup rows per
-// routed expert on average (the 8192-row window: ~160), so that a group takes
-// two tiles instead of three (gate/up) or four (down) and its weights are
-// dequantised that much less often; the blocks then run two per CU instead of
-// three (gate/up) and one instead of two (down).  The shared expert's down
-// takes them above kTallRowsPerGroup rows of its own.
+// Tall gate/up and down tiles: for calls whose routed experts average more
+// rows than one tile of the usual height holds (64 gate/up, 48 down: from
+// about 3072 rows at 512 experts top-10), so that a group takes fewer tiles
+// and its weights are dequantised that much less often; the blocks then run
+// two per CU instead of three (gate/up) and one instead of two (down).  The
+// shared expert's down takes them above 48 rows of its own.
 #ifndef VM_GROUPED_ROWS_TALL
 #define VM_GROUPED_ROWS_TALL 96
 #endif
 constexpr int kGroupedRowsTall = VM_GROUPED_ROWS_TALL;
-constexpr uint32_t kTallRowsPerGroup = 128;
 constexpr int kGroupedRowsDown = VM_GROUPED_ROWS_DN;
 constexpr int kGroupedRowsRouter = VM_GROUPED_ROWS_RT;  // router GEMM tiles (no sort: rows in order)
 constexpr uint32_t kNoRow = 0xffffffffu;  // pair without a row (invalid expert id)
