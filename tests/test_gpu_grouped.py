@@ -92,8 +92,9 @@ def test_grouped_layer_small(device, tokens):
 
 @pytest.mark.parametrize("tokens", [130, 300])
 def test_grouped_layer_narrow_hidden_with_shared_expert(device, tokens):
-    """Hidden 256 with a shared expert above 64 rows: the shared expert runs
-    on the side stream and the combine reads its rows and sigmoid gates back.
+    """Hidden 256 with a shared expert: at 130 rows one more group of the
+    sorted GEMMs, at 300 rows on the side stream, whose rows and sigmoid gates
+    the combine reads back.
     At this width a token's 32 combine threads share a wave with another
     token's, so the combine takes its per-lane loads (wider layers read a
     token's indices, scores and gate through scalar loads)."""

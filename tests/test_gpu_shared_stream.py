@@ -1,8 +1,10 @@
-"""The shared expert of grouped calls above 64 rows runs on a second stream of
-the calling thread (forked from the caller's stream before the router GEMM,
-joined back before the combine).  vm_moe_layer_static never creates that
-stream, so it takes the one-stream path, where the shared expert is one more
-group of the sorted GEMMs: the two entry points must give the same bits.  The
+"""The shared expert of grouped calls above 256 rows runs on a second stream
+of the calling thread (forked from the caller's stream before the router
+GEMM, joined back before the combine).  vm_moe_layer_static never creates
+that stream, so it takes the one-stream path, where the shared expert is one
+more group of the sorted GEMMs, as every grouped call of up to 256 rows does:
+the two entry points must give the same bits (65 rows: both one-stream; 257
+and 777 rows: the side stream against the one-stream path).  The
 fork and join must also hold inside a captured HIP graph: every replay, with
 eager calls between the replays, equals the eager call on the same input."""
 import ctypes
@@ -33,7 +35,7 @@ def _call(layer, x, entry):
     return out, inds, scores
 
 
-@pytest.mark.parametrize("tokens", [65, 200, 777])
+@pytest.mark.parametrize("tokens", [65, 257, 777])
 def test_side_stream_shared_expert_equals_the_one_stream_path(device, tokens):
     layer = assemble.build_layer(SPEC, SEED, device, dense=True)
     need = _lib.lib().vm_moe_layer_workspace(tokens, SPEC.top_k, SPEC.hidden, SPEC.inter, SPEC.shared_inter,

@@ -605,6 +605,14 @@ static bool use_grouped(uint32_t T, uint32_t dtype) { return T > VM_LAYER_MAX_TO
 // router row per wave over every token); above, the router is an MFMA GEMM.
 constexpr uint32_t kFrontMaxTokens = 64;
 
+// Calls above this many rows run the shared expert on a side stream beside the
+// router GEMM, the selection and the sort.  Its fork and join cost the caller's
+// stream about 6 us each, which smaller calls do not win back: with the shared
+// expert as one more group of the sorted GEMMs, 96 rows took 86 us instead of
+// 93 and 256 rows 117 instead of 120, while 512 rows took 288 instead of 283
+// and 2048 rows 386 instead of 382.
+constexpr uint32_t kSideMinTokens = 256;
+
 uint64_t vm_moe_layer_workspace(uint32_t tokens, uint32_t top_k, uint32_t hidden_size, uint32_t inter_size,
                                 uint32_t shared_inter, uint32_t expert_count, uint32_t act_dtype) {
   if (use_grouped(tokens, act_dtype))
@@ -1250,11 +1258,11 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
   // count and one layout + scatter launch.
   const bool counted = T > kFrontMaxTokens && uint64_t(T) * K > vm::kSortOneBlockPairs &&
                        (phases & VM_PHASE_ROUTER) && (phases & VM_PHASE_EXPERTS);
-  // Calls that take the router GEMM run the shared expert on the side stream,
+  // Calls above kSideMinTokens rows run the shared expert on the side stream,
   // into the last T rows of the activation and expert-row buffers (the routed
   // rows take at most the first T * K).
   SideStream* side = nullptr;
-  if (shared && T > kFrontMaxTokens && (phases & VM_PHASE_ROUTER) && (phases & VM_PHASE_EXPERTS))
+  if (shared && T > kSideMinTokens && (phases & VM_PHASE_ROUTER) && (phases & VM_PHASE_EXPERTS))
     side = side_stream(stream);
   uint16_t* sh_rows = reinterpret_cast<uint16_t*>(ws + w.rows) + uint64_t(T) * K * H;
   if (side != nullptr) {
