@@ -25,11 +25,12 @@ OpenMP) on a bounded sample of tokens, on this host's cores.
 Extra fields (not `value`): "decode_small" (hidden 1024 / inter 256 / 64
 experts top-4 at batch 1 over 256 layers, with the NumPy oracle's time per
 token); "batched" (32 rows per call, Zipf(1.1) routing, 8 pool-resident
-layers cycled) and "prefill" (2048 rows per call, 3 layers cycled) through
+layers cycled) and "prefill" (2048 rows per call, 8 layers cycled) through
 the grouped path: rows/s, algorithmic GB/s and the bf16 MFMA fraction
 (algorithmic FLOPs / time / 2.5 PFLOP/s); "prefill_window" (the layer-major
 order: four 2048-row chunks in one layer call, each expert read once per
-window); "stack48_lru" (48 layers at batch 1 with a 3,051-slot LRU pool,
+window); "row_sweep" (µs per call of grouped calls of 96 and 256 rows at the
+batched routing and 512, 1024 and 4096 rows at the prefill shape); "stack48_lru" (48 layers at batch 1 with a 3,051-slot LRU pool,
 Zipf routing, misses staged from pinned host memory): tokens/s through the
 stack, hit rate, staged bytes; "custom_executor" with --custom-executor
 module:attr (the reference harness's plug-in convention).
@@ -730,6 +731,8 @@ def main():
     parser.add_argument("--no-stack", action="store_true",
                         help="skip the 48-layer stack with the LRU pool and host-staged misses")
     parser.add_argument("--no-small", action="store_true", help="skip the small decode layer (hidden 1024)")
+    parser.add_argument("--no-sweep", action="store_true",
+                        help="skip the grouped calls of 96-4096 rows between the batched and prefill shapes")
     parser.add_argument("--no-branch", action="store_true", help="skip the decoder MLP branch")
     parser.add_argument("--custom-executor", "--executor", "--custom", dest="custom", default=None,
                         help="module:attr of an executor to validate and time beside this package's "
@@ -828,6 +831,16 @@ def main():
         log("layer-major prefill window: four 2048-row chunks per layer call")
         result["prefill_window"] = run_grouped("prefill", 8192, 4, 10, args.seed)
         result["prefill_window"]["window"] = "4 chunks x 2048 rows in one layer call (layer-major order)"
+    if not args.no_grouped and not args.no_sweep:
+        log("grouped calls between the batched and prefill shapes")
+        sweep = {"note": "µs per layer call by wall clock; batched_*: the batched configuration's Zipf(1.1) "
+                         "routing at more rows, prefill_*: the prefill configuration at fewer or more rows"}
+        for name, tokens, layers, reps in (("batched", 96, 8, 30), ("batched", 256, 8, 30), ("prefill", 512, 8, 20),
+                                           ("prefill", 1024, 8, 20), ("prefill", 4096, 4, 10)):
+            r = run_grouped(name, tokens, layers, reps, args.seed)
+            sweep[f"{name}_{tokens}"] = {"us_per_call": r["us_per_layer"], "tok_s": r["tok_s"],
+                                         "distinct_experts": r["distinct_experts"], "kernels_us": r["kernels_us"]}
+        result["row_sweep"] = sweep
     if not args.no_stack:
         log("48-layer stack, LRU pool of 6 GB, misses from pinned host")
         # the stated Zipf(1.1) recipe, and its logit bias scaled to reach the ~60% hit rate
