@@ -1321,11 +1321,6 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
             ? vm::launch_router_gemm(r, stream)
             : vm::launch_grouped(vm::kEpiLogits, r, (T + vm::kGroupedRowsRouter - 1) / vm::kGroupedRowsRouter, stream);
     if (e != hipSuccess) return done(hip_fail(e, "router launch"));
-    if (shared && side == nullptr) {
-      e = vm::launch_shared_gate(static_cast<const uint16_t*>(a->x), to_ptrs(a->shared_expert_gate), sig, T, H,
-                                 stream);
-      if (e != hipSuccess) return done(hip_fail(e, "shared gate launch"));
-    }
   }
   if (phases & VM_PHASE_ROUTER) {
     // softmax / top-k / renorm per row
@@ -1339,6 +1334,13 @@ static int layer_grouped(const VmLayerArgs* a, hipStream_t stream) {
     s.act_dtype = VM_BF16;
     s.blend = a->renorm_blend;
     s.gates = phases == VM_PHASE_ROUTER ? a->gates_out : nullptr;
+    if (shared && side == nullptr && T > kFrontMaxTokens) {
+      // the shared expert as a sorted group: its sigmoid gate by the selection's waves
+      s.gate_x = static_cast<const uint16_t*>(a->x);
+      s.seg = to_ptrs(a->shared_expert_gate);
+      s.shared_sig = sig;
+      s.hidden = H;
+    }
     e = vm::launch_select(s, stream);
     if (e != hipSuccess) return done(hip_fail(e, "select launch"));
   }

@@ -61,7 +61,7 @@ constexpr int kGateupRowsPerLane = VM_GATEUP_ROWS;
 #endif
 constexpr int kGuWaves = VM_GATEUP_WAVES;  // waves per gate/up block
 constexpr int kGuBlock = kGuWaves * 64;
-template <class A>
+template <class A, bool GATE = false>
 __device__ void select_body(const SelectLaunch& p) {
   __shared__ typename Cand<A>::T s_cand[kMaxCand];
   const uint32_t t = blockIdx.x;
@@ -69,6 +69,11 @@ __device__ void select_body(const SelectLaunch& p) {
   GateKeys<A> g;
   float lg[kMaxExpertsPerLane];
   load_logits(p.logits + static_cast<size_t>(t) * p.experts, p.experts, lane, lg);
+  if constexpr (GATE) {  // its loads go out with the logits'
+    static_assert(std::is_same_v<A, ActBF16>, "the shared gate of bf16 grouped calls");
+    const float logit = shared_gate_logit_bf16(p.gate_x + static_cast<size_t>(t) * p.hidden, p.seg, p.hidden, lane);
+    if (lane == 0) ActBF16::store(p.shared_sig, t, sigmoid_act<ActBF16>(logit));
+  }
   softmax_keys<A>(lg, p.experts, lane, g);
   if (p.gates != nullptr) {
     void* gates = static_cast<char*>(p.gates) + static_cast<size_t>(t) * p.experts * A::kBytes;
@@ -88,6 +93,9 @@ __device__ void select_body(const SelectLaunch& p) {
 }
 
 __global__ __launch_bounds__(64) void k_select_bf16(SelectLaunch p) { select_body<ActBF16>(p); }
+// with the shared expert's sigmoid gate of each token (an instance of its own:
+// the gate's registers would cost the plain selection a wave per SIMD)
+__global__ __launch_bounds__(64) void k_select_bf16_gate(SelectLaunch p) { select_body<ActBF16, true>(p); }
 __global__ __launch_bounds__(64) void k_select_f32(SelectLaunch p) { select_body<ActF32>(p); }
 
 // A decode call over a device-LRU pool: wave t selects the experts of token t
@@ -699,6 +707,10 @@ hipError_t launch_select_lru(const SelectLaunch& p, const LruLaunch& l, hipStrea
 
 hipError_t launch_select(const SelectLaunch& p, hipStream_t stream) {
   const dim3 grid(p.tokens), block(64);
+  if (p.seg.w != nullptr) {
+    if (p.act_dtype != 0) return hipErrorInvalidValue;
+    return launch("select", k_select_bf16_gate, grid, block, stream, p);
+  }
   return p.act_dtype == 0 ? launch("select", k_select_bf16, grid, block, stream, p)
                           : launch("select", k_select_f32, grid, block, stream, p);
 }

@@ -1463,22 +1463,8 @@ __global__ __launch_bounds__(kGB) void k_grouped_combine(CombineLaunch p) {
 
 // sigmoid(round(x . dequant(seg))) per token, one wave per token (bf16).
 __global__ __launch_bounds__(64) void k_shared_gate(const uint16_t* x, ProjPtrs seg, uint16_t* sig, uint32_t hidden) {
-  const uint32_t t = blockIdx.x, lane = threadIdx.x, G = hidden / kGroup;
-  float acc = 0.0f;
-  for (uint32_t g = lane; g < G; g += 64) {
-    const uint4 w = ldg16(seg.w + g * kWordsPerGroup);
-    const uint16_t* src = x + static_cast<size_t>(t) * hidden + g * kGroup;
-    uint32_t raw[16], xp[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 v = ldg16(src + 8 * i);
-      raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
-    }
-    pair_activations(raw, xp);
-    const float sum = bf16_pair_sum(raw);
-    acc += fmaf(bf16_to_f32(seg.s[g]), q4_dot_bf16(w, xp) - 128.0f * sum, bf16_to_f32(seg.b[g]) * sum);
-  }
-  const float logit = round_bf16(wave_sum_all(acc));
+  const uint32_t t = blockIdx.x, lane = threadIdx.x;
+  const float logit = shared_gate_logit_bf16(x + static_cast<size_t>(t) * hidden, seg, hidden, lane);
   if (lane == 0) ActBF16::store(sig, t, sigmoid_act<ActBF16>(logit));
 }
 

@@ -272,6 +272,30 @@ struct ProjPtrs {
   const uint16_t* b;
 };
 
+// The shared expert's H -> 1 Q4 gate logit of one bf16 row, summed by one
+// wave and rounded to bf16: the grouped path's shared gate kernel and the
+// selection of calls that run the shared expert as a sorted group use this
+// one sum.
+__device__ __forceinline__ float shared_gate_logit_bf16(const uint16_t* x_row, const ProjPtrs& seg, uint32_t hidden,
+                                                        uint32_t lane) {
+  const uint32_t G = hidden / kGroup;
+  float acc = 0.0f;
+  for (uint32_t g = lane; g < G; g += 64) {
+    const uint4 w = ldg16(seg.w + g * kWordsPerGroup);
+    const uint16_t* src = x_row + g * kGroup;
+    uint32_t raw[16], xp[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint4 v = ldg16(src + 8 * i);
+      raw[4 * i] = v.x; raw[4 * i + 1] = v.y; raw[4 * i + 2] = v.z; raw[4 * i + 3] = v.w;
+    }
+    pair_activations(raw, xp);
+    const float sum = bf16_pair_sum(raw);
+    acc += fmaf(bf16_to_f32(seg.s[g]), q4_dot_bf16(w, xp) - 128.0f * sum, bf16_to_f32(seg.b[g]) * sum);
+  }
+  return round_bf16(wave_sum_all(acc));
+}
+
 struct PoolDev {
   const uint8_t* base;
   uint64_t header;

@@ -35,6 +35,12 @@ struct SelectLaunch {
   uint32_t tokens, experts, top_k;
   int act_dtype;
   float blend;
+  // optional (bf16 grouped calls whose shared expert is a sorted group): the
+  // shared expert's sigmoid gate of each token, computed by the same wave
+  const uint16_t* gate_x;      // [T, hidden]
+  ProjPtrs seg;                // H -> 1 Q4 gate row; seg.w null: none
+  uint16_t* shared_sig;        // [T]
+  uint32_t hidden;
 };
 
 // K2: gate/up + SwiGLU of every (token, slot) pair and the shared pairs.
