@@ -524,7 +524,18 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
   // the three terms occupy disjoint bits, so the step's part is XORed on last
   const uint32_t a_lane = am * kRowB + ((akb * 4) ^ (kSwz ? a_swz(am) : 0u)) * 16;
   const uint32_t w_lane = (bkb ^ w_swz(bn)) * 16;  // the group part of the weight-line reads
+  // The gate/up waves raise their issue priority (s_setprio, a wave's own
+  // scheduling priority on its SIMD) while they compute a chunk.  Three blocks
+  // share a CU, each in its own phase; with the raise the SIMD prefers the
+  // waves whose dequantisation and MFMAs are ready over those of a block that
+  // is issuing its next loads or storing them to LDS.  Same instructions, same
+  // bits; on three boxes the 2048-row gate/up took 193.5-208.9 -> 191.5-201.5
+  // us and the 8192-row window's 503-545 -> 488-527 us.  The raise during the
+  // LDS-store phase instead, a higher level (2 or 3), or the same raise in the
+  // down GEMM gained nothing consistent.
+  constexpr bool kPrio = EPI == kEpiSwiglu;
   auto compute = [&](int buf, const BChunk<Q4, TAIL> (&bc)[PROJ][NBW]) {
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(1);
     const uint8_t* s_a = s_a0 + buf * kStage;
     BChunk<Q4, TAIL> bl[PROJ][NBW];
     uint32_t s2[PROJ][NBW], b2[PROJ][NBW];
@@ -573,6 +584,7 @@ __device__ __forceinline__ void grouped_tile(const GroupedLaunch& p, const ProjP
             acc[pj][nb][mb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[mb], bop, acc[pj][nb][mb], 0, 0, 0);
         }
     }
+    if constexpr (kPrio) __builtin_amdgcn_s_setprio(0);
   };
   // only a K that is not a multiple of the chunk has a tail chunk
   auto tail_chunk = [&](uint32_t c) { return TAIL && (c + 1) * kCG > G; };
